@@ -1,0 +1,24 @@
+// Host-side helpers shared by the C-ABI translation units (error channel, launch checks).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/physllm_moe.h"
+
+namespace physllm {
+
+// Records (code, message) as the calling thread's last error and returns code.
+int set_error(int code, const char* msg);
+// Clears the calling thread's last error and returns PHYSLLM_MOE_OK.
+int ok();
+// Checks hipGetLastError() after a launch; records ELAUNCH with `what` on failure.
+int check_launch(const char* what);
+
+int dequant_launch(const void* packed, const void* scales, void* out, int64_t numel, int block_size,
+                   hipStream_t stream);
+int router_launch(const void* x, const void* w, const void* bias, int B, int H, int E, int K, void* idx,
+                  void* wts, hipStream_t stream);
+
+}  // namespace physllm

@@ -1,0 +1,201 @@
+// Host side of the C ABI: error channel, workspace carving and the whole-layer
+// entry point (the MoE half of crates/llm-core/src/moe.rs:246-307 without the
+// host round trips of :261-299 — routing stays on the device, so one layer is a
+// fixed sequence of asynchronous launches on the caller's stream).
+#include <stdio.h>
+#include <string.h>
+
+#include "capi_internal.h"
+#include "experts.h"
+
+namespace physllm {
+
+static thread_local int t_err_code = 0;
+static thread_local char t_err_msg[256] = {0};
+
+int set_error(int code, const char* msg) {
+    t_err_code = code;
+    snprintf(t_err_msg, sizeof(t_err_msg), "%s", msg ? msg : "");
+    return code;
+}
+
+int ok() {
+    t_err_code = 0;
+    t_err_msg[0] = 0;
+    return PHYSLLM_MOE_OK;
+}
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        char buf[256];
+        snprintf(buf, sizeof(buf), "%s: %s", what, hipGetErrorString(e));
+        return set_error(PHYSLLM_MOE_ELAUNCH, buf);
+    }
+    return ok();
+}
+
+// Workspace regions, each 256-byte aligned.
+struct Workspace {
+    int32_t* idx;
+    float* wts;
+    int32_t* counts;
+    int32_t* offsets;
+    int32_t* active;
+    int32_t* n_active;
+    int32_t* perm;
+    int32_t* pos;
+    uint16_t* h;
+    float* y;
+    size_t bytes;
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static Workspace carve(const physllm_moe_config& c, int B, char* base) {
+    const size_t N = (size_t)B * c.top_k;
+    const size_t E = (size_t)c.num_experts;
+    Workspace w;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        char* p = base ? base + o : nullptr;
+        o += align256(bytes);
+        return p;
+    };
+    w.idx = (int32_t*)take(N * 4);
+    w.wts = (float*)take(N * 4);
+    w.counts = (int32_t*)take(E * 4);
+    w.offsets = (int32_t*)take((E + 1) * 4);
+    w.active = (int32_t*)take(E * 4);
+    w.n_active = (int32_t*)take(4);
+    w.perm = (int32_t*)take(N * 4);
+    w.pos = (int32_t*)take(N * 4);
+    w.h = (uint16_t*)take(N * (size_t)c.intermediate * 2);
+    w.y = (float*)take(N * (size_t)c.hidden * 4);
+    w.bytes = o;
+    return w;
+}
+
+static int validate(const physllm_moe_config* c, int B) {
+    if (!c) return set_error(PHYSLLM_MOE_EINVAL, "layer: null config");
+    if (c->hidden < 32 || c->hidden % 32) return set_error(PHYSLLM_MOE_EINVAL, "layer: hidden must be a positive multiple of 32");
+    if (c->intermediate < 32 || c->intermediate % 32)
+        return set_error(PHYSLLM_MOE_EINVAL, "layer: intermediate must be a positive multiple of 32");
+    if (c->num_experts < 1 || c->num_experts > 1024) return set_error(PHYSLLM_MOE_EINVAL, "layer: num_experts must be in [1, 1024]");
+    if (c->top_k < 1 || c->top_k > c->num_experts || c->top_k > 32)
+        return set_error(PHYSLLM_MOE_EINVAL, "layer: top_k must be in [1, min(num_experts, 32)]");
+    if (B < 0) return set_error(PHYSLLM_MOE_EINVAL, "layer: batch < 0");
+    if ((int64_t)B * c->top_k > (1LL << 28)) return set_error(PHYSLLM_MOE_EINVAL, "layer: batch * top_k too large");
+    return PHYSLLM_MOE_OK;
+}
+
+}  // namespace physllm
+
+using namespace physllm;
+
+extern "C" int physllm_moe_last_error(void) { return t_err_code; }
+extern "C" const char* physllm_moe_last_error_message(void) { return t_err_msg; }
+
+extern "C" size_t physllm_moe_workspace_bytes(const physllm_moe_config* cfg, int batch) {
+    if (validate(cfg, batch) != PHYSLLM_MOE_OK) return 0;
+    ok();
+    return carve(*cfg, batch, nullptr).bytes;
+}
+
+// Stages of one layer over a shared workspace. Bit i of `stages` runs stage i:
+// 0 route (router + bucketing), 1 gate_up (+ SwiGLU), 2 down, 3 combine.
+enum { kStageRoute = 1, kStageGateUp = 2, kStageDown = 4, kStageCombine = 8, kStageAll = 15 };
+
+static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* w, const void* x, int batch,
+                      void* out, void* topk_idx, void* topk_w, void* workspace, size_t workspace_bytes,
+                      hipStream_t s, int stages) {
+    int rc = validate(cfg, batch);
+    if (rc) return rc;
+    if (batch == 0) return ok();
+    const physllm_moe_config& c = *cfg;
+    if ((stages & (kStageRoute | kStageGateUp | kStageDown)) &&
+        (!w || !w->router_w || !w->gate_up_blocks || !w->gate_up_scales || !w->down_blocks || !w->down_scales))
+        return set_error(PHYSLLM_MOE_EINVAL, "layer: null weight pointer");
+    if ((stages & (kStageRoute | kStageGateUp)) && !x) return set_error(PHYSLLM_MOE_EINVAL, "layer: null x");
+    if ((stages & kStageCombine) && !out) return set_error(PHYSLLM_MOE_EINVAL, "layer: null out");
+    const size_t need = carve(c, batch, nullptr).bytes;
+    if (!workspace || workspace_bytes < need) return set_error(PHYSLLM_MOE_EWORKSPACE, "layer: workspace too small");
+    Workspace ws = carve(c, batch, (char*)workspace);
+    const int N = batch * c.top_k;
+    int32_t* idx = topk_idx ? (int32_t*)topk_idx : ws.idx;
+    float* wts = topk_w ? (float*)topk_w : ws.wts;
+
+    if (stages & kStageRoute) {
+        if ((rc = router_launch(x, w->router_w, w->router_b, batch, c.hidden, c.num_experts, c.top_k, idx, wts, s)))
+            return rc;
+        if ((rc = bucket_launch(idx, N, c.num_experts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.active,
+                                ws.n_active, s)))
+            return rc;
+    }
+    const int max_slots = N < c.num_experts ? N : c.num_experts;
+    GemvParams p{};
+    p.counts = ws.counts;
+    p.offsets = ws.offsets;
+    p.perm = ws.perm;
+    p.active = ws.active;
+    p.n_active = ws.n_active;
+    p.top_k = c.top_k;
+    p.alpha = c.swiglu_alpha;
+    p.limit = c.swiglu_limit;
+    if (stages & kStageGateUp) {
+        p.act = (const uint16_t*)x;
+        p.blocks = (const uint8_t*)w->gate_up_blocks;
+        p.scales = (const uint8_t*)w->gate_up_scales;
+        p.bias = (const uint16_t*)w->gate_up_bias;
+        p.out = ws.h;
+        p.Kdim = c.hidden;
+        p.R = 2 * c.intermediate;
+        if ((rc = gemv_launch(kModeGateUp, p, max_slots, batch, s))) return rc;
+    }
+    if (stages & kStageDown) {
+        p.act = ws.h;
+        p.blocks = (const uint8_t*)w->down_blocks;
+        p.scales = (const uint8_t*)w->down_scales;
+        p.bias = (const uint16_t*)w->down_bias;
+        p.out = ws.y;
+        p.Kdim = c.intermediate;
+        p.R = c.hidden;
+        if ((rc = gemv_launch(kModeDown, p, max_slots, batch, s))) return rc;
+    }
+    if (stages & kStageCombine) {
+        if ((rc = combine_launch(ws.y, ws.pos, wts, (uint16_t*)out, batch, c.hidden, c.top_k, s))) return rc;
+    }
+    return ok();
+}
+
+extern "C" int physllm_moe_layer_forward(const physllm_moe_config* cfg, const physllm_moe_weights* w,
+                                         const void* x, int batch, void* out, void* topk_idx, void* topk_w,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+    return run_stages(cfg, w, x, batch, out, topk_idx, topk_w, workspace, workspace_bytes, (hipStream_t)stream,
+                      kStageAll);
+}
+
+extern "C" int physllm_moe_stage_route(const physllm_moe_config* cfg, const physllm_moe_weights* w, const void* x,
+                                       int batch, void* topk_idx, void* topk_w, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+    return run_stages(cfg, w, x, batch, nullptr, topk_idx, topk_w, workspace, workspace_bytes, (hipStream_t)stream,
+                      kStageRoute);
+}
+
+extern "C" int physllm_moe_stage_gate_up(const physllm_moe_config* cfg, const physllm_moe_weights* w, const void* x,
+                                         int batch, void* workspace, size_t workspace_bytes, void* stream) {
+    return run_stages(cfg, w, x, batch, nullptr, nullptr, nullptr, workspace, workspace_bytes, (hipStream_t)stream,
+                      kStageGateUp);
+}
+
+extern "C" int physllm_moe_stage_down(const physllm_moe_config* cfg, const physllm_moe_weights* w, int batch,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+    return run_stages(cfg, w, nullptr, batch, nullptr, nullptr, nullptr, workspace, workspace_bytes,
+                      (hipStream_t)stream, kStageDown);
+}
+
+extern "C" int physllm_moe_stage_combine(const physllm_moe_config* cfg, int batch, void* out, const void* topk_w,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+    return run_stages(cfg, nullptr, nullptr, batch, out, nullptr, (void*)topk_w, workspace, workspace_bytes,
+                      (hipStream_t)stream, kStageCombine);
+}

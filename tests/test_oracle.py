@@ -1,0 +1,264 @@
+"""Pins the C oracle (oracle/moe_oracle.c) against independently derived answers.
+
+The reference ships no tests or golden vectors for this path, so each oracle
+function is checked against mathematics that fixes its answer: exact rational
+e2m1/E8M0 decoding, hand-built index vectors, float64 brute force with its own
+decoder, closed-form SwiGLU points, and permutation invariants.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from physllm_amd import synthetic as syn
+from tests import refmath
+
+
+# ---- dequant -------------------------------------------------------------------
+
+def test_dequant_kat_exhaustive(oracle):
+    """All 16 codes x 256 E8M0 scales against exact rational RNE (incl. subnormal,
+    overflow to inf, -0.0 for code 8, NaN for scale 255)."""
+    kat = refmath.mxfp4_kat()
+    got = np.array([[oracle.mxfp4_value_bf16(c, s) for c in range(16)] for s in range(256)], dtype=np.uint16)
+    bad = np.argwhere(got != kat)
+    assert bad.size == 0, f"first mismatches (scale, code): {bad[:8].tolist()}"
+    # spot checks written by hand
+    assert kat[127, 1] == 0x3F00      # 0.5
+    assert kat[127, 7] == 0x40C0      # 6.0
+    assert kat[127, 8] == 0x8000      # -0.0
+    assert kat[127, 15] == 0xC0C0     # -6.0
+    assert kat[120, 2] == 0x3C00      # 1 * 2^-7
+    assert kat[0, 1] == 0x0020        # 0.5 * 2^-127 = 2^-128, subnormal
+    assert kat[254, 4] == 0x7F80      # 2 * 2^127 overflows to +inf
+    assert kat[254, 3] == 0x7F40      # 1.5 * 2^127 is finite
+
+
+def test_dequant_matches_kat_through_flat_tensor(oracle, golden_kat=None):
+    """Every byte value under every scale through or_mxfp4_dequant (block 32)."""
+    kat = refmath.mxfp4_kat()
+    # 256 scales x 256 bytes: block j has scale j//16... arrange 16 bytes (=1 block) per scale
+    bytes_all = np.arange(256, dtype=np.uint8)
+    packed = np.tile(bytes_all, 256)                 # 65536 bytes = 4096 blocks of 16 bytes
+    scales = np.repeat(np.arange(256, dtype=np.uint8), 16)  # each scale covers 16 blocks = 256 bytes
+    out = oracle.mxfp4_dequant(packed, scales, packed.size * 2)
+    s_of_byte = np.repeat(np.arange(256), 256)
+    b = packed.astype(np.int64)
+    exp = np.stack([kat[s_of_byte, b & 15], kat[s_of_byte, b >> 4]], axis=1).reshape(-1)
+    assert np.array_equal(out, exp)
+
+
+def test_dequant_nibble_order_and_block_index_by_hand(oracle):
+    # two blocks: scale 127 (x1) then 128 (x2); byte 0x21 -> [code 1, code 2] = [0.5, 1.0]
+    packed = np.zeros(32, dtype=np.uint8)
+    packed[0] = 0x21
+    packed[15] = 0x7F          # elements 30, 31 -> codes 15 (-6), 7 (6)
+    packed[16] = 0x90          # element 32 -> code 0 (0), element 33 -> code 9 (-0.5)
+    scales = np.array([127, 128], dtype=np.uint8)
+    out = oracle.mxfp4_dequant(packed, scales, 64)
+    assert out[0] == 0x3F00 and out[1] == 0x3F80          # 0.5, 1.0
+    assert out[30] == 0xC0C0 and out[31] == 0x40C0        # -6, 6 at scale 1
+    assert out[32] == 0x0000 and out[33] == 0xBF80        # 0, -0.5*2 = -1.0 at scale 2
+    assert np.all(out[2:30] == 0)
+
+
+def test_dequant_odd_block_size_uses_even_element_scale(oracle):
+    """kernels/mxfp4_dequant.hip:43 indexes the scale by element 2i for both nibbles."""
+    packed = np.array([0x22, 0x22, 0x22], dtype=np.uint8)   # all codes 2 (=1.0)
+    scales = np.array([127, 128], dtype=np.uint8)            # block_size 3 -> elements 0-2, 3-5
+    out = oracle.mxfp4_dequant(packed, scales, 6, block_size=3)
+    # pairs (0,1): scale of 0 -> 1.0; pair (2,3): scale of 2 (block 0) -> 1.0 for BOTH
+    # (element 3 alone would be block 1); pair (4,5): block 1 -> 2.0
+    assert out.tolist() == [0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x4000, 0x4000]
+
+
+def test_dequant_odd_numel(oracle):
+    packed = np.array([0x21, 0x43], dtype=np.uint8)
+    out = oracle.mxfp4_dequant(packed, np.array([127], np.uint8), 3)
+    assert out.tolist() == [0x3F00, 0x3F80, 0x3FC0]
+
+
+# ---- router --------------------------------------------------------------------
+
+def _rand_bits(rng, shape, sigma):
+    return syn.bf16_from_f32(rng.standard_normal(shape, dtype=np.float32) * np.float32(sigma))
+
+
+@pytest.mark.parametrize("B,H,E,K", [(5, 64, 8, 2), (17, 2880, 32, 4), (9, 320, 128, 4)])
+def test_router_matches_float64_bruteforce(oracle, B, H, E, K):
+    rng = np.random.default_rng(B * 1000 + E)
+    x = _rand_bits(rng, (B, H), 1.0)
+    w = _rand_bits(rng, (E, H), 0.02)
+    b = _rand_bits(rng, (E,), 0.02)
+    idx, wts, lg = oracle.router(x, w, b, K, return_logits=True)
+    ref_lg = refmath.bf16_bits_to_f64(x) @ refmath.bf16_bits_to_f64(w).T + refmath.bf16_bits_to_f64(b)
+    assert np.allclose(lg, ref_lg, rtol=0, atol=1e-12)
+    ref_idx = refmath.topk_desc_stable(ref_lg, K)
+    assert np.array_equal(idx, ref_idx)
+    sel = np.take_along_axis(ref_lg, ref_idx, 1)
+    ex = np.exp(sel - sel.max(1, keepdims=True))
+    assert np.allclose(wts, ex / ex.sum(1, keepdims=True), rtol=1e-6, atol=1e-7)
+    assert np.allclose(wts.sum(1), 1.0, atol=1e-6)
+    assert np.all(np.diff(wts, axis=1) <= 0)
+
+
+def test_topk_ties_nan_and_order(oracle):
+    idx, w = oracle.topk_softmax([1.0, 3.0, 3.0, 2.0, 3.0], 3)
+    assert idx.tolist() == [1, 2, 4]                       # ties -> lowest index first
+    assert np.allclose(w, [1 / 3] * 3)
+    idx, w = oracle.topk_softmax([np.nan, 0.5, np.nan, -1.0], 3)
+    assert idx.tolist() == [1, 3, 0]                       # NaN ranks below every number
+    assert math.isnan(w[2])
+    idx, _ = oracle.topk_softmax([-np.inf, -np.inf, -np.inf], 2)
+    assert idx.tolist() == [0, 1]                          # distinct indices, lowest first
+    idx, w = oracle.topk_softmax([0.0, math.log(3.0)], 2)
+    assert idx.tolist() == [1, 0] and np.allclose(w, [0.75, 0.25], rtol=1e-7)
+
+
+def test_router_agrees_with_reference_fp32_arithmetic(oracle):
+    """The reference accumulates in fp32, serially (moe_router.hip:25-35). Its top-k
+    equals the oracle's (no bias) wherever the k/k+1 gap exceeds the fp32 error
+    bound n*u*sum|x_d w_d|, which covers all but a vanishing fraction of tokens."""
+    rng = np.random.default_rng(7)
+    B, H, E, K = 64, 2880, 32, 4
+    x = _rand_bits(rng, (B, H), 1.0)
+    w = _rand_bits(rng, (E, H), 0.02)
+    idx, _ = oracle.router(x, w, None, K)
+    lg32 = oracle.router_logits_fp32_serial(x, w)
+    absum = np.abs(refmath.bf16_bits_to_f64(x)) @ np.abs(refmath.bf16_bits_to_f64(w)).T
+    bound = H * 2.0 ** -24 * absum.max(1)
+    checked = 0
+    for t in range(B):
+        s = np.sort(lg32[t].astype(np.float64))[::-1]
+        if s[K - 1] - s[K] > 2 * bound[t]:
+            checked += 1
+            ref = refmath.topk_desc_stable(lg32[t:t + 1].astype(np.float64), K)[0]
+            assert set(ref.tolist()) == set(idx[t].tolist())
+    assert checked >= B // 2
+
+
+# ---- bucketing -----------------------------------------------------------------
+
+@pytest.mark.parametrize("B,K,E", [(1, 4, 32), (64, 4, 32), (300, 4, 128), (7, 2, 3)])
+def test_bucket_is_stable_counting_sort(oracle, B, K, E):
+    rng = np.random.default_rng(B + E)
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(B)]).astype(np.int32)
+    counts, offsets, perm, pos = oracle.bucket(idx, E)
+    flat = idx.reshape(-1)
+    assert np.array_equal(counts, np.bincount(flat, minlength=E))
+    assert offsets[0] == 0 and np.array_equal(np.diff(offsets), counts) and offsets[-1] == B * K
+    assert np.array_equal(perm, np.argsort(flat, kind="stable"))
+    assert np.array_equal(pos[perm], np.arange(B * K))
+
+
+def test_bucket_all_tokens_one_expert(oracle):
+    idx = np.zeros((10, 1), dtype=np.int32)
+    counts, offsets, perm, pos = oracle.bucket(idx, 4)
+    assert counts.tolist() == [10, 0, 0, 0] and offsets.tolist() == [0, 10, 10, 10, 10]
+    assert perm.tolist() == list(range(10))
+
+
+# ---- SwiGLU --------------------------------------------------------------------
+
+def test_swiglu_closed_forms(oracle):
+    a = 1.702
+    g34 = math.log(3.0) / a                       # sigmoid(a g) = 3/4 exactly
+    assert oracle.swiglu(g34, 1.0) == pytest.approx(g34 * 0.75 * 2.0, rel=1e-6)
+    for u in (-8.0, -7.0, 0.0, 7.0, 8.0, 100.0):
+        assert oracle.swiglu(0.0, u) == 0.0      # g = 0 kills the output
+    for g in (-3.0, 0.5, 9.0):
+        assert oracle.swiglu(g, -1.0) == 0.0     # (u + 1) = 0
+    # clamps: g above the limit acts as the limit; u is clamped on both sides
+    assert oracle.swiglu(8.0, 3.0) == oracle.swiglu(7.0, 3.0)
+    assert oracle.swiglu(2.0, 8.0) == oracle.swiglu(2.0, 7.0)
+    assert oracle.swiglu(2.0, -50.0) == oracle.swiglu(2.0, -7.0)
+    assert oracle.swiglu(-9.0, 0.0) != oracle.swiglu(-7.0, 0.0)   # no lower clamp on g
+    assert oracle.swiglu(7.0, 7.0) == pytest.approx(7.0 / (1 + math.exp(-a * 7.0)) * 8.0, rel=1e-6)
+    assert math.isnan(oracle.swiglu(float("nan"), 1.0))
+    assert math.isnan(oracle.swiglu(1.0, float("nan")))
+
+
+# ---- expert / layer ------------------------------------------------------------
+
+def _tiny_layer(seed=3, E=4, H=64, I=64, K=2, zipf=None, bias=True):
+    return syn.make_layer(E, H, I, K, seed=seed, zipf=zipf, with_bias=bias)
+
+
+@pytest.mark.parametrize("bias", [True, False])
+def test_layer_matches_float64_bruteforce(oracle, bias):
+    layer = _tiny_layer(bias=bias)
+    x = syn.make_x(3, 64, seed=11)
+    r = oracle.moe_layer(layer, x, want_pairs=True)
+    ref_out, ref_idx, ref_w = refmath.moe_layer_f64(layer, x)
+    assert np.array_equal(r["idx"], ref_idx)
+    assert np.allclose(r["wts"], ref_w, rtol=1e-6)
+    got = refmath.bf16_bits_to_f64(r["out"])
+    assert refmath.rel_l2(got, ref_out) < 4e-3
+    # a dropped bias, a swapped gate/up or a wrong scale would be O(1) off
+    assert np.max(np.abs(got - ref_out)) <= 8 * 2.0 ** -8 * np.max(np.abs(ref_out))
+
+
+def test_layer_larger_shape_bruteforce(oracle):
+    layer = syn.make_layer(8, 256, 128, 3, seed=5)
+    x = syn.make_x(20, 256, seed=6)
+    r = oracle.moe_layer(layer, x)
+    ref_out, ref_idx, _ = refmath.moe_layer_f64(layer, x)
+    assert np.array_equal(r["idx"], ref_idx)
+    assert refmath.rel_l2(refmath.bf16_bits_to_f64(r["out"]), ref_out) < 4e-3
+
+
+def test_layer_thread_count_invariance(oracle):
+    layer = syn.make_layer(8, 128, 64, 2, seed=9)
+    x = syn.make_x(13, 128, seed=9)
+    a = oracle.moe_layer(layer, x, nthreads=1)
+    b = oracle.moe_layer(layer, x, nthreads=5)
+    assert np.array_equal(a["out"], b["out"]) and np.array_equal(a["idx"], b["idx"])
+
+
+def test_experts_pairs_views_consistent(oracle):
+    layer = _tiny_layer()
+    x = syn.make_x(3, 64, seed=2)
+    r = oracle.moe_layer(layer, x, want_pairs=True)
+    # out = bf16(sum_j w_j y_j) recomputed from the pair views
+    y = r["y_pairs"].reshape(3, 2, 64).astype(np.float64)
+    comb = (r["wts"][:, :, None] * y).sum(1)
+    assert refmath.rel_l2(refmath.bf16_bits_to_f64(r["out"]), comb) < 4e-3
+
+
+# ---- legacy single-token path ---------------------------------------------------
+
+def test_legacy_expert_and_combine_bruteforce(oracle):
+    rng = np.random.default_rng(1)
+    H, I, K = 96, 64, 3
+    x = _rand_bits(rng, (H,), 1.0)
+    wg = _rand_bits(rng, (I, H), 0.05)
+    wu = _rand_bits(rng, (I, H), 0.05)
+    wd = _rand_bits(rng, (H, I), 0.05)
+    inter = oracle.legacy_expert_silu(x, wg, wu)
+    xf = refmath.bf16_bits_to_f64(x)
+    g = refmath.bf16_bits_to_f64(wg) @ xf
+    u = refmath.bf16_bits_to_f64(wu) @ xf
+    ref_inter = g / (1 + np.exp(-g)) * u
+    assert refmath.rel_l2(refmath.bf16_bits_to_f64(inter), ref_inter) < 4e-3
+    y = oracle.legacy_expert_down(inter, wd)
+    ref_y = refmath.bf16_bits_to_f64(wd) @ refmath.bf16_bits_to_f64(inter)
+    assert refmath.rel_l2(refmath.bf16_bits_to_f64(y), ref_y) < 4e-3
+    ys = _rand_bits(rng, (K, H), 1.0)
+    wk = np.array([0.5, 0.3, 0.2], dtype=np.float32)
+    out = oracle.legacy_combine(ys, wk)
+    ref = (wk[:, None].astype(np.float64) * refmath.bf16_bits_to_f64(ys)).sum(0)
+    assert refmath.rel_l2(refmath.bf16_bits_to_f64(out), ref) < 4e-3
+
+
+def test_synthetic_distributions():
+    layer = syn.make_layer(4, 64, 64, 2, seed=1, zipf=1.1)
+    assert layer.gate_up_scales.min() >= 119 and layer.gate_up_scales.max() <= 123
+    assert set(np.unique(layer.down_scales).tolist()) <= set(range(119, 124))
+    assert layer.gate_up_blocks.shape == (4, 128, 32) and layer.down_blocks.shape == (4, 64, 32)
+    # seeded: identical bytes on every call
+    again = syn.make_layer(4, 64, 64, 2, seed=1, zipf=1.1)
+    assert np.array_equal(layer.gate_up_blocks, again.gate_up_blocks)
+    assert np.array_equal(layer.router_b, again.router_b)
+    # per-expert algorithmic bytes for the GPT-OSS shape (13,236,480 B)
+    big = syn.MoELayer(2880, 2880, 1, 4, *[None] * 8)
+    assert big.expert_bytes == 13_236_480

@@ -8,30 +8,34 @@ namespace physllm {
 
 enum { kModeGateUp = 0, kModeDown = 1 };
 
-// One grouped-expert pass over routed tokens. The expert of work slot s is
-// active[s] (s < *n_active); its tokens are the sorted positions
-// offsets[e] .. offsets[e] + counts[e].
+// One grouped-expert pass over routed tokens. Work slot s covers the s-th touched
+// expert (ascending id); its tokens are the sorted positions
+// slots[s].z .. slots[s].z + slots[s].y.
 struct GemvParams {
     const uint16_t* act;     // gate_up: x [B, Kdim] (row = pair / top_k); down: h [N, Kdim] by sorted position
     const uint8_t* blocks;   // [E, R, Kdim/2] packed e2m1
     const uint8_t* scales;   // [E, R, Kdim/32] E8M0
     const uint16_t* bias;    // [E, R] bf16, nullable
-    const int32_t* counts;   // [E]
-    const int32_t* offsets;  // [E+1]
     const int32_t* perm;     // [N] sorted position -> pair id
-    const int32_t* active;   // [E] touched experts, ascending
-    const int32_t* n_active; // [1]
+    const int4* slots;       // [E] {expert, tokens, first sorted position, 0}; tokens = 0 past the touched ones
+    const int32_t* n_slots;  // [1] number of touched experts
     void* out;               // gate_up: h bf16 [N, R/2]; down: y fp32 [N, R] (by sorted position)
+    int act_rows;            // rows of act (gate_up: batch; down: N)
     int Kdim;                // reduction length (H for gate_up, I for down)
     int R;                   // weight rows per expert (2I or H)
     int top_k;
+    int split;               // K splits (down only; partials at out + s * n_pairs * R)
+    int n_pairs;             // N = batch * top_k
+    int rt;                  // row-tile sets per workgroup (set by the launcher)
     float alpha, limit;
 };
 
+constexpr int kMaxSplit = 4;
+
 int gemv_launch(int mode, const GemvParams& p, int max_slots, int max_tokens, hipStream_t stream);
-int combine_launch(const float* y, const int32_t* pos, const float* wts, uint16_t* out, int B, int H, int K,
-                   hipStream_t stream);
-int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, void* perm, void* pos, void* active,
-                  void* n_active, hipStream_t stream);
+int combine_launch(const float* y, int nsplit, size_t split_stride, const int32_t* pos, const float* wts,
+                   uint16_t* out, int B, int H, int K, hipStream_t stream);
+int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, void* perm, void* pos, void* slots,
+                  void* n_slots, hipStream_t stream);
 
 }  // namespace physllm

@@ -29,98 +29,322 @@
 
 namespace physllm {
 
-constexpr int kGemvChunk = 8;  // k-steps (4 MX blocks each) prefetched per chunk
+constexpr int kGemvThreads = 256;  // 4 waves, each one 16-row weight tile at a time
+constexpr int kGemvNit = 23;       // k-steps of 4 MX blocks held in registers: 92 blocks = 2944 elements
+constexpr int kPassTok = 8;        // tokens staged in LDS per pass
+constexpr int kStageU = 4;         // 16-byte activation loads in flight per thread while staging
+constexpr int kMaxScaleBlocks = 256;  // K <= 8192: a tile's scales (16 x NB bytes) fit a wave's LDS slice
 
+// Stages activation rows for tokens [tb, tb + ntok) and MX blocks [sb0, sb1) into
+// LDS as xs[r][c] (c in 16-byte units, row stride su = 4 * (sb1 - sb0) + 1: the
+// one-unit pad spreads the 16 token rows of a B-fragment read over the banks).
 template <int MODE>
-__global__ __launch_bounds__(512) void k_mx_gemv(GemvParams p) {
-    extern __shared__ uint4 lds_act[];  // [16][Kdim + 8] bf16, in 16-byte units
-    const int slot = blockIdx.y;
-    if (slot >= *p.n_active) return;
-    const int e = p.active[slot];
-    const int ne = p.counts[e];
-    const int p0 = p.offsets[e];
-    const int nwaves = blockDim.x >> 6;
+__device__ __forceinline__ void gemv_stage(const GemvParams& p, uint4* xs, int p0, int tb, int ntok, int sb0,
+                                           int sb1, int su) {
+    const int cu = (sb1 - sb0) * 4;  // 16-byte units per row in this segment
+    const int units = ntok * cu;
+    for (int i0 = threadIdx.x; i0 < units; i0 += kGemvThreads * kStageU) {
+        uint4 v[kStageU];
+#pragma unroll
+        for (int u = 0; u < kStageU; ++u) {
+            const int i = i0 + u * kGemvThreads;
+            v[u] = make_uint4(0, 0, 0, 0);
+            if (i < units) {
+                const int r = i / cu, c = i - r * cu;
+                const int q = tb + r;
+                const size_t arow = (MODE == kModeGateUp) ? (size_t)(p.perm[p0 + q] / p.top_k) : (size_t)(p0 + q);
+                v[u] = ((const uint4*)(p.act + arow * (size_t)p.Kdim))[sb0 * 4 + c];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kStageU; ++u) {
+            const int i = i0 + u * kGemvThreads;
+            if (i < units) {
+                const int r = i / cu, c = i - r * cu;
+                xs[r * su + c] = v[u];
+            }
+        }
+    }
+}
+
+// Generic form (any K up to 8192, several row-tile sets per group). Grid: x =
+// groups of `rt` row-tile sets (a set = 4 waves x 16 rows), y = expert work slot,
+// z = K split. Per row tile, a wave
+//   1. fetches the tile's 16 x NB scale bytes with at most 4 wide loads into its
+//      own LDS slice (one 16-byte load per lane, not one byte load per k-step:
+//      the memory pipeline is bound by load instructions, not bytes);
+//   2. loads its 16 rows over the split's K range into registers (up to 23
+//      k-steps, 16 bytes per lane each = 16 rows x 64 contiguous bytes per wave;
+//      longer K ranges run in segments);
+//   3. runs every 8-token pass of the expert's tokens against the registers:
+//      heavy experts cost extra activation reads and MFMA issue, not extra HBM
+//      traffic.
+// The activations of a pass are staged once per group in LDS and reused by all
+// of the group's row tiles when the expert has at most 8 tokens. Four
+// accumulators break the MFMA dependency chain; they are summed in a fixed order.
+template <int MODE>
+__global__ __launch_bounds__(kGemvThreads) void k_mx_gemv_generic(GemvParams p) {
+    extern __shared__ uint4 lds[];
+    const int4 si = p.slots[blockIdx.y];  // {expert, tokens, first sorted position, 0}
+    const int e = si.x, ne = si.y, p0 = si.z;
+    if (ne <= 0) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r0 = (blockIdx.x * nwaves + wave) * 16;
-    const bool wave_active = r0 < p.R;
     const int m = lane & 15, g = lane >> 4;
     const int NB = p.Kdim >> 5;
-    const int nit = (NB + 3) >> 2;
-    const int ldsu = (p.Kdim >> 3) + 1;  // LDS row stride in uint4 (16 B pad per row)
-    const size_t row = (size_t)e * p.R + (wave_active ? r0 + m : 0);
-    const uint4* wrow = (const uint4*)(p.blocks + row * (size_t)(p.Kdim >> 1));
-    const uint8_t* srow = p.scales + row * (size_t)NB;
-    const int u4_row = p.Kdim >> 3;
+    const int split = blockIdx.z;
+    const int per = (NB + p.split - 1) / p.split;
+    const int kb0 = min(NB, split * per);
+    const int kb1 = min(NB, kb0 + per);
+    const int seg_blocks = 4 * kGemvNit;
+    const int nseg = (kb1 - kb0 + seg_blocks - 1) / seg_blocks;
+    const int su = 4 * min(kb1 - kb0, seg_blocks) + 1;
+    const int npass = (ne + kPassTok - 1) / kPassTok;
+    const bool restage = npass > 1 || nseg > 1;  // else: one staging serves every tile
 
-    for (int tb = 0; tb < ne; tb += 16) {
-        const int ntok = min(16, ne - tb);
-        __syncthreads();
-        for (int i = threadIdx.x; i < ntok * u4_row; i += blockDim.x) {
-            const int r = i / u4_row, c = i - r * u4_row;
-            const uint16_t* src;
-            if (MODE == kModeGateUp) {
-                const int pair = p.perm[p0 + tb + r];
-                src = p.act + (size_t)(pair / p.top_k) * p.Kdim;
-            } else {
-                src = p.act + (size_t)(p0 + tb + r) * p.Kdim;
-            }
-            lds_act[r * ldsu + c] = ((const uint4*)src)[c];
-        }
-        __syncthreads();
-        if (!wave_active) continue;
+    uint8_t* scl = (uint8_t*)lds + wave * 16 * NB;           // this wave's tile scales [16][NB]
+    uint4* xs = lds + (4 * 16 * NB) / 16;                     // activations [kPassTok][su]
+    const int sc_units = NB;  // 16 * NB bytes = NB 16-byte units
 
-        const bool tv = m < ntok;
-        const uint4* xl = lds_act + m * ldsu;
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-
-        // Ping-pong chunk buffers: chunk c+1's loads are in flight while chunk c computes.
-        uint4 qa[kGemvChunk], qb[kGemvChunk];
-        uint32_t sa[kGemvChunk], sb[kGemvChunk];
-        auto load_chunk = [&](uint4 (&q)[kGemvChunk], uint32_t (&s)[kGemvChunk], int c0) {
+    uint4 wq[kGemvNit];
+    for (int it = 0; it < p.rt; ++it) {
+        const int r0 = ((blockIdx.x * p.rt + it) * (kGemvThreads / 64) + wave) * 16;
+        if (r0 >= p.R) break;  // wave-uniform; later tiles are past the end too
+        const size_t row0 = (size_t)e * p.R + r0;
+        const uint4* wrow = (const uint4*)(p.blocks + (row0 + m) * (size_t)(p.Kdim >> 1));
+        const uint4* scg = (const uint4*)(p.scales + row0 * (size_t)NB);
+        uint4 sv[kMaxScaleBlocks / 64];
 #pragma unroll
-            for (int j = 0; j < kGemvChunk; ++j) {
-                const int blk = (c0 + j) * 4 + g;
-                const bool bv = blk < NB;
-                q[j] = bv ? wrow[blk] : make_uint4(0, 0, 0, 0);
-                s[j] = bv ? (uint32_t)srow[blk] : 127u;
+        for (int u = 0; u < kMaxScaleBlocks / 64; ++u)
+            sv[u] = (lane + 64 * u < sc_units) ? scg[lane + 64 * u] : make_uint4(0, 0, 0, 0);
+        auto load_w = [&](int sb0, int sb1) {
+#pragma unroll
+            for (int j = 0; j < kGemvNit; ++j) {
+                const int blk = sb0 + 4 * j + g;
+                wq[j] = blk < sb1 ? wrow[blk] : make_uint4(0, 0, 0, 0);
             }
         };
-        auto compute_chunk = [&](const uint4 (&q)[kGemvChunk], const uint32_t (&s)[kGemvChunk], int c0) {
+        if (nseg == 1) load_w(kb0, kb1);
 #pragma unroll
-            for (int j = 0; j < kGemvChunk; ++j) {
-                if (c0 + j >= nit) break;
-                const int blk = (c0 + j) * 4 + g;
-                const float sf = e8m0_scale_operand(s[j]);
-                const bf16x8_t a0 = mx_cvt8(q[j].x, sf);
-                const bf16x8_t a1 = mx_cvt8(q[j].y, sf);
-                const bf16x8_t a2 = mx_cvt8(q[j].z, sf);
-                const bf16x8_t a3 = mx_cvt8(q[j].w, sf);
-                uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0, x2 = x0, x3 = x0;
-                if (tv && blk < NB) {
-                    x0 = xl[blk * 4 + 0];
-                    x1 = xl[blk * 4 + 1];
-                    x2 = xl[blk * 4 + 2];
-                    x3 = xl[blk * 4 + 3];
+        for (int u = 0; u < kMaxScaleBlocks / 64; ++u)
+            if (lane + 64 * u < sc_units) ((uint4*)scl)[lane + 64 * u] = sv[u];
+
+        for (int tb = 0; tb < ne; tb += kPassTok) {
+            const int ntok = min(kPassTok, ne - tb);
+            const bool tv = m < ntok;
+            f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+            for (int sg = 0; sg < nseg; ++sg) {
+                const int sb0 = kb0 + sg * seg_blocks;
+                const int sb1 = min(kb1, sb0 + seg_blocks);
+                if (nseg > 1) load_w(sb0, sb1);
+                if (restage || it == 0) {
+                    // every wave of the group reaches this point together: tiles past the
+                    // end only occur on the group's last iteration, where all waves stop
+                    __syncthreads();  // previous pass/segment finished reading xs
+                    gemv_stage<MODE>(p, xs, p0, tb, ntok, sb0, sb1, su);
+                    __syncthreads();
                 }
-                acc = mfma16x16x32(a0, as_bf16x8(x0), acc);
-                acc = mfma16x16x32(a1, as_bf16x8(x1), acc);
-                acc = mfma16x16x32(a2, as_bf16x8(x2), acc);
-                acc = mfma16x16x32(a3, as_bf16x8(x3), acc);
+                const uint4* xl = xs + m * su;
+                const uint8_t* sl = scl + m * NB;
+#pragma unroll
+                for (int j = 0; j < kGemvNit; ++j) {
+                    const int lb = 4 * j + g;  // block index within the segment
+                    if (sb0 + 4 * j < sb1) {   // wave-uniform
+                        const bool bv = sb0 + lb < sb1;
+                        uint32_t sj = sl[sb0 + (bv ? lb : 0)];
+                        // decode inside the pass loop: an opaque no-op on the scale keeps the
+                        // compiler from hoisting 23 x 16 VGPRs of converted fragments
+                        asm volatile("" : "+v"(sj));
+                        const float sf = e8m0_scale_operand(sj);
+                        uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0, x2 = x0, x3 = x0;
+                        if (tv && bv) {
+                            x0 = xl[lb * 4 + 0];
+                            x1 = xl[lb * 4 + 1];
+                            x2 = xl[lb * 4 + 2];
+                            x3 = xl[lb * 4 + 3];
+                        }
+                        acc0 = mfma16x16x32(mx_cvt8(wq[j].x, sf), as_bf16x8(x0), acc0);
+                        acc1 = mfma16x16x32(mx_cvt8(wq[j].y, sf), as_bf16x8(x1), acc1);
+                        acc2 = mfma16x16x32(mx_cvt8(wq[j].z, sf), as_bf16x8(x2), acc2);
+                        acc3 = mfma16x16x32(mx_cvt8(wq[j].w, sf), as_bf16x8(x3), acc3);
+                    }
+                }
             }
-        };
-        load_chunk(qa, sa, 0);
-        for (int c0 = 0; c0 < nit; c0 += 2 * kGemvChunk) {
-            load_chunk(qb, sb, c0 + kGemvChunk);
-            compute_chunk(qa, sa, c0);
-            load_chunk(qa, sa, c0 + 2 * kGemvChunk);
-            compute_chunk(qb, sb, c0 + kGemvChunk);
+            if (!tv) continue;
+            const f32x4_t acc = (acc0 + acc1) + (acc2 + acc3);
+            const int pp = p0 + tb + m;  // sorted position of this lane's token
+            const int rr = r0 + 4 * g;
+            float bsum[4] = {0.f, 0.f, 0.f, 0.f};
+            if (p.bias && split == 0) {
+                const uint2 bb = *(const uint2*)(p.bias + (size_t)e * p.R + rr);
+                bsum[0] = bf16_lo(bb.x);
+                bsum[1] = bf16_hi(bb.x);
+                bsum[2] = bf16_lo(bb.y);
+                bsum[3] = bf16_hi(bb.y);
+            }
+            if (MODE == kModeGateUp) {
+                const float h0 = swiglu(acc[0] + bsum[0], acc[1] + bsum[1], p.alpha, p.limit);
+                const float h1 = swiglu(acc[2] + bsum[2], acc[3] + bsum[3], p.alpha, p.limit);
+                const int I = p.R >> 1;
+                uint32_t* hout = (uint32_t*)((uint16_t*)p.out + (size_t)pp * I + (rr >> 1));
+                *hout = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
+            } else {
+                float4 y;
+                y.x = acc[0] + bsum[0];
+                y.y = acc[1] + bsum[1];
+                y.z = acc[2] + bsum[2];
+                y.w = acc[3] + bsum[3];
+                float* ybase = (float*)p.out + (size_t)split * p.n_pairs * p.R;
+                *(float4*)(ybase + (size_t)pp * p.R + rr) = y;
+            }
         }
+    }
+}
 
-        if (!tv) continue;
+// Buffer resource (V#) for raw buffer loads on gfx9-family GPUs: `bytes` of
+// range-checked memory from `base`; loads past the range return zeros, so tile
+// edges need no clamped (per-load) addresses and the k-step of a load is an
+// immediate offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, int imm) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff + (uint32_t)imm, 0, 0);
+}
+
+// Fast form for K ranges of at most 92 MX blocks (2944 elements: GPT-OSS H = I =
+// 2880 = 90 blocks), one 16-row tile per wave, loads in this order:
+//   1. the expert slot (scalar load), then the wave's 23 weight stripes (16
+//      bytes per lane each: 16 rows x 64 contiguous bytes per wave) and the
+//      tile's scales (two 16-byte loads per lane) — the bulk of the bytes is in
+//      flight after a single dependent load;
+//   2. the first pass's token rows (scalar loads of the sorted pair ids) and the
+//      activation units this thread stages (NS 16-byte loads).
+// Everything is then stored to LDS once, one barrier, and the 23 k-steps run
+// from registers and LDS. Experts with more than 8 tokens
+// run further passes against the same registers.
+template <int MODE, int NS>
+__global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p) {
+    extern __shared__ uint4 lds[];
+    const int4 si = p.slots[blockIdx.y];  // {expert, tokens, first sorted position, 0}
+    const int e = si.x, ne = si.y, p0 = si.z;
+    if (ne <= 0) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int m = lane & 15, g = lane >> 4;
+    const int NB = p.Kdim >> 5;
+    const int split = blockIdx.z;
+    const int per = (NB + p.split - 1) / p.split;
+    const int kb0 = min(NB, split * per);
+    const int nblk = min(NB, kb0 + per) - kb0;  // <= 92
+    const int cu = nblk * 4;                    // 16-byte activation units per token row
+    const int su = cu + 1;                      // LDS row stride (one-unit pad)
+    const int r0 = (blockIdx.x * (kGemvThreads / 64) + wave) * 16;
+    const uint32_t row_bytes = (uint32_t)(p.Kdim >> 1);
+    const uint32_t exp_w = (uint32_t)p.R * row_bytes;   // one expert's codes
+    const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;  // one expert's scales
+
+    uint8_t* scl = (uint8_t*)lds + wave * 16 * 96;  // this wave's tile scales [16][NB <= 92]
+    uint4* xs = lds + (4 * 16 * 96) / 16;          // activations [kPassTok][su]
+
+    // ---- 1. weights and scales (rows past R read zeros) ----
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.blocks + (size_t)e * exp_w, exp_w);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales + (size_t)e * exp_s, exp_s);
+    const uint32_t woff = (uint32_t)(r0 + m) * row_bytes + (uint32_t)(kb0 + g) * 16u;
+    u32x4_t wq[kGemvNit];
+#pragma unroll
+    for (int j = 0; j < kGemvNit; ++j) wq[j] = buf_load16(rw, woff, 64 * j);
+    const uint32_t soff = (uint32_t)r0 * NB + lane * 16u;  // 16 rows x NB bytes, contiguous
+    const u32x4_t sv0 = buf_load16(rs, soff, 0);
+    const u32x4_t sv1 = buf_load16(rs, soff, 1024);
+
+    // ---- 2. activations of pass 0 ----
+    const __amdgpu_buffer_rsrc_t ract = make_rsrc(p.act, (uint32_t)p.act_rows * (uint32_t)p.Kdim * 2u);
+    auto stage_load = [&](int tb, u32x4_t (&v)[NS]) {
+        // lane r < kPassTok holds the activation row of pass row r (scalar loads of
+        // the sorted pair ids, then one register); units fetch theirs by shuffle
+        int rowid = 0;
+#pragma unroll
+        for (int r = 0; r < kPassTok; ++r) {
+            const int q = min(tb + r, ne - 1);
+            const int id = (MODE == kModeGateUp) ? p.perm[p0 + q] / p.top_k : p0 + q;
+            rowid = (lane == r) ? id : rowid;
+        }
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            const int i = threadIdx.x + u * kGemvThreads;
+            const int r = i / cu, c = i - r * cu;
+            const int row = __shfl(rowid, r & (kPassTok - 1), 64);
+            const uint32_t off = (uint32_t)row * (uint32_t)(p.Kdim * 2) + (uint32_t)(kb0 * 4 + c) * 16u;
+            v[u] = buf_load16(ract, off, 0);
+        }
+    };
+    auto stage_store = [&](int ntok, const u32x4_t (&v)[NS]) {
+        const int units = ntok * cu;
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            const int i = threadIdx.x + u * kGemvThreads;
+            if (i < units) {
+                const int r = i / cu, c = i - r * cu;
+                ((u32x4_t*)xs)[r * su + c] = v[u];
+            }
+        }
+    };
+    int ntok = min(kPassTok, ne);
+    {
+        u32x4_t xv[NS];
+        stage_load(0, xv);
+        __builtin_amdgcn_sched_barrier(0);
+        if (lane < NB) ((u32x4_t*)scl)[lane] = sv0;
+        if (lane + 64 < NB) ((u32x4_t*)scl)[lane + 64] = sv1;
+        stage_store(ntok, xv);
+    }
+    __syncthreads();
+
+    const bool row_ok = r0 < p.R;
+    for (int tb = 0; tb < ne; tb += kPassTok) {
+        if (tb > 0) {
+            ntok = min(kPassTok, ne - tb);
+            u32x4_t xn[NS];
+            stage_load(tb, xn);
+            __syncthreads();  // every wave finished reading the previous pass
+            stage_store(ntok, xn);
+            __syncthreads();
+        }
+        // lane's column of the B fragment at block 4j+g; lanes past the pass's tokens
+        // read a valid row (an MFMA output column depends only on its own B column,
+        // and those columns are not stored)
+        const uint4* xl = xs + min(m, ntok - 1) * su + 4 * g;
+        const uint8_t* sl = scl + m * NB + kb0 + g;
+        f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+#pragma unroll
+        for (int j = 0; j < kGemvNit; ++j) {
+            if (4 * j < nblk) {  // wave-uniform
+                const bool edge = 4 * j + 3 >= nblk;  // wave-uniform: some lanes past the K range
+                const bool bv = 4 * j + g < nblk;
+                uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
+                // decode inside the pass loop: an opaque no-op on the scale keeps the
+                // compiler from hoisting 23 x 16 VGPRs of converted fragments
+                asm volatile("" : "+v"(sj));
+                const float sf = e8m0_scale_operand(sj);
+                u32x4_t q = wq[j];
+                uint4 x0 = xl[16 * j + 0], x1 = xl[16 * j + 1], x2 = xl[16 * j + 2], x3 = xl[16 * j + 3];
+                if (edge && !bv) {
+                    q = u32x4_t{0u, 0u, 0u, 0u};
+                    x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
+                }
+                acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
+                acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
+                acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
+                acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
+            }
+        }
+        const bool tv = m < ntok;
+        if (!row_ok || !tv) continue;
+        const f32x4_t acc = (acc0 + acc1) + (acc2 + acc3);
         const int pp = p0 + tb + m;  // sorted position of this lane's token
         const int rr = r0 + 4 * g;
         float bsum[4] = {0.f, 0.f, 0.f, 0.f};
-        if (p.bias) {
+        if (p.bias && split == 0) {
             const uint2 bb = *(const uint2*)(p.bias + (size_t)e * p.R + rr);
             bsum[0] = bf16_lo(bb.x);
             bsum[1] = bf16_hi(bb.x);
@@ -139,16 +363,19 @@ __global__ __launch_bounds__(512) void k_mx_gemv(GemvParams p) {
             y.y = acc[1] + bsum[1];
             y.z = acc[2] + bsum[2];
             y.w = acc[3] + bsum[3];
-            *(float4*)((float*)p.out + (size_t)pp * p.R + rr) = y;
+            float* ybase = (float*)p.out + (size_t)split * p.n_pairs * p.R;
+            *(float4*)(ybase + (size_t)pp * p.R + rr) = y;
         }
     }
 }
 
 // out[t, d] = bf16( sum_j w[t,j] * y[pos[t*k+j], d] ), fp32 fma in k order
-// (kernels/moe_combine.hip:16-20, batched). Each lane handles 4 consecutive d.
+// (kernels/moe_combine.hip:16-20, batched). With a K-split down projection, y is
+// the sum of the split partials, added in split order first. Each lane handles 4
+// consecutive d.
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, const int32_t* __restrict__ pos,
                                                  const float* __restrict__ wts, uint16_t* __restrict__ out, int H,
-                                                 int K) {
+                                                 int K, int nsplit, size_t split_stride) {
     const int t = blockIdx.y;
     const int d4 = blockIdx.x * 256 + threadIdx.x;
     if (d4 * 4 >= H) return;
@@ -156,7 +383,14 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, co
     for (int j = 0; j < K; ++j) {
         const int q = pos[(size_t)t * K + j];
         const float w = wts[(size_t)t * K + j];
-        const float4 v = ((const float4*)(y + (size_t)q * H))[d4];
+        float4 v = ((const float4*)(y + (size_t)q * H))[d4];
+        for (int sp = 1; sp < nsplit; ++sp) {
+            const float4 u = ((const float4*)(y + sp * split_stride + (size_t)q * H))[d4];
+            v.x += u.x;
+            v.y += u.y;
+            v.z += u.z;
+            v.w += u.w;
+        }
         acc.x = __builtin_fmaf(w, v.x, acc.x);
         acc.y = __builtin_fmaf(w, v.y, acc.y);
         acc.z = __builtin_fmaf(w, v.z, acc.z);
@@ -168,38 +402,57 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, co
     ((uint2*)(out + (size_t)t * H))[d4] = o;
 }
 
-static size_t gemv_lds_bytes(int kdim, int max_tokens) {
-    return (size_t)max_tokens * ((size_t)(kdim >> 3) + 1) * 16;
-}
-
-int gemv_launch(int mode, const GemvParams& p, int max_slots, int max_tokens, hipStream_t stream) {
+int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, hipStream_t stream) {
+    GemvParams p = p0;
+    if (p.split < 1 || p.split > kMaxSplit) return set_error(PHYSLLM_MOE_EINVAL, "gemv: bad split");
+    const int NB = p.Kdim >> 5;
+    if (NB > kMaxScaleBlocks) return set_error(PHYSLLM_MOE_EINVAL, "gemv: reduction dimension > 8192");
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)k_mx_gemv<kModeGateUp>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024);
-        (void)hipFuncSetAttribute((const void*)k_mx_gemv<kModeDown>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024);
+        const void* ks[] = {(const void*)k_mx_gemv<kModeGateUp, 2>, (const void*)k_mx_gemv<kModeGateUp, 12>,
+                            (const void*)k_mx_gemv<kModeDown, 2>, (const void*)k_mx_gemv<kModeDown, 12>,
+                            (const void*)k_mx_gemv_generic<kModeGateUp>, (const void*)k_mx_gemv_generic<kModeDown>};
+        for (const void* k : ks) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr_set = true;
     }
-    const int ntok = max_tokens < 16 ? max_tokens : 16;
-    const size_t lds = gemv_lds_bytes(p.Kdim, ntok);
-    if (lds > 160 * 1024) return set_error(PHYSLLM_MOE_EINVAL, "gemv: reduction dimension too large for LDS");
-    // One token: many small groups (4 waves) so every CU gets work; more tokens: 8
-    // waves share the staged activations.
-    const int waves = ntok <= 4 ? 4 : 8;
-    const int rows_per_group = waves * 16;
-    dim3 grid((p.R + rows_per_group - 1) / rows_per_group, max_slots);
-    if (mode == kModeGateUp)
-        hipLaunchKernelGGL(k_mx_gemv<kModeGateUp>, grid, dim3(waves * 64), lds, stream, p);
-    else
-        hipLaunchKernelGGL(k_mx_gemv<kModeDown>, grid, dim3(waves * 64), lds, stream, p);
+    const int per = (NB + p.split - 1) / p.split;
+    const int ntok = max_tokens < kPassTok ? max_tokens : kPassTok;
+    const int rows_per_set = (kGemvThreads / 64) * 16;
+    const int sets = (p.R + rows_per_set - 1) / rows_per_set;
+    if (per <= 4 * kGemvNit) {
+        // activation units one thread stages per pass: ntok rows x 4*per 16-byte units
+        const int units = ntok * 4 * per;
+        const int ns = (units + kGemvThreads - 1) / kGemvThreads;
+        const size_t lds = (size_t)4 * 16 * 96 + (size_t)kPassTok * (4 * per + 1) * 16;
+        dim3 grid(sets, max_slots, p.split);
+        p.rt = 1;
+        if (ns <= 2) {
+            if (mode == kModeGateUp) hipLaunchKernelGGL((k_mx_gemv<kModeGateUp, 2>), grid, dim3(kGemvThreads), lds, stream, p);
+            else hipLaunchKernelGGL((k_mx_gemv<kModeDown, 2>), grid, dim3(kGemvThreads), lds, stream, p);
+        } else {
+            if (mode == kModeGateUp) hipLaunchKernelGGL((k_mx_gemv<kModeGateUp, 12>), grid, dim3(kGemvThreads), lds, stream, p);
+            else hipLaunchKernelGGL((k_mx_gemv<kModeDown, 12>), grid, dim3(kGemvThreads), lds, stream, p);
+        }
+    } else {
+        const int seg = 4 * kGemvNit;
+        const size_t lds = (size_t)4 * 16 * NB + (size_t)ntok * (4 * seg + 1) * 16;
+        const long total = (long)sets * max_slots * p.split;
+        int rt = (int)(total / 1024);
+        rt = rt < 1 ? 1 : (rt > 8 ? 8 : rt);
+        p.rt = rt;
+        dim3 grid((sets + rt - 1) / rt, max_slots, p.split);
+        if (mode == kModeGateUp)
+            hipLaunchKernelGGL(k_mx_gemv_generic<kModeGateUp>, grid, dim3(kGemvThreads), lds, stream, p);
+        else
+            hipLaunchKernelGGL(k_mx_gemv_generic<kModeDown>, grid, dim3(kGemvThreads), lds, stream, p);
+    }
     return check_launch(mode == kModeGateUp ? "gate_up gemv" : "down gemv");
 }
 
-int combine_launch(const float* y, const int32_t* pos, const float* wts, uint16_t* out, int B, int H, int K,
-                   hipStream_t stream) {
+int combine_launch(const float* y, int nsplit, size_t split_stride, const int32_t* pos, const float* wts,
+                   uint16_t* out, int B, int H, int K, hipStream_t stream) {
     dim3 grid((H / 4 + 255) / 256, B);
-    hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, stream, y, pos, wts, out, H, K);
+    hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, stream, y, pos, wts, out, H, K, nsplit, split_stride);
     return check_launch("combine");
 }
 

@@ -5,6 +5,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "capi_internal.h"
 #include "experts.h"
 
@@ -41,16 +43,28 @@ struct Workspace {
     float* wts;
     int32_t* counts;
     int32_t* offsets;
-    int32_t* active;
-    int32_t* n_active;
+    int4* slots;
+    int32_t* n_slots;
     int32_t* perm;
     int32_t* pos;
     uint16_t* h;
-    float* y;
+    float* y;     // [split][N][H]
+    int split;
     size_t bytes;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// K splits of the down projection: enough 16-row work tiles (one per wave) to
+// cover the chip when few experts are touched (decode at small batch).
+static int down_split(const physllm_moe_config& c, int B) {
+    const int64_t slots = std::min<int64_t>((int64_t)B * c.top_k, c.num_experts);
+    const int64_t tiles = slots * ((c.hidden + 15) / 16);
+    const int64_t want = 2048;
+    int split = (int)std::min<int64_t>(kMaxSplit, (want + tiles - 1) / std::max<int64_t>(tiles, 1));
+    split = std::max(1, std::min(split, c.intermediate / 32));
+    return split;
+}
 
 static Workspace carve(const physllm_moe_config& c, int B, char* base) {
     const size_t N = (size_t)B * c.top_k;
@@ -66,12 +80,13 @@ static Workspace carve(const physllm_moe_config& c, int B, char* base) {
     w.wts = (float*)take(N * 4);
     w.counts = (int32_t*)take(E * 4);
     w.offsets = (int32_t*)take((E + 1) * 4);
-    w.active = (int32_t*)take(E * 4);
-    w.n_active = (int32_t*)take(4);
+    w.slots = (int4*)take(E * 16);
+    w.n_slots = (int32_t*)take(4);
     w.perm = (int32_t*)take(N * 4);
     w.pos = (int32_t*)take(N * 4);
     w.h = (uint16_t*)take(N * (size_t)c.intermediate * 2);
-    w.y = (float*)take(N * (size_t)c.hidden * 4);
+    w.split = down_split(c, B);
+    w.y = (float*)take((size_t)w.split * N * (size_t)c.hidden * 4);
     w.bytes = o;
     return w;
 }
@@ -128,22 +143,22 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
     if (stages & kStageRoute) {
         if ((rc = router_launch(x, w->router_w, w->router_b, batch, c.hidden, c.num_experts, c.top_k, idx, wts, s)))
             return rc;
-        if ((rc = bucket_launch(idx, N, c.num_experts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.active,
-                                ws.n_active, s)))
+        if ((rc = bucket_launch(idx, N, c.num_experts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.slots, ws.n_slots, s)))
             return rc;
     }
     const int max_slots = N < c.num_experts ? N : c.num_experts;
     GemvParams p{};
-    p.counts = ws.counts;
-    p.offsets = ws.offsets;
     p.perm = ws.perm;
-    p.active = ws.active;
-    p.n_active = ws.n_active;
+    p.slots = ws.slots;
+    p.n_slots = ws.n_slots;
     p.top_k = c.top_k;
+    p.split = 1;
+    p.n_pairs = N;
     p.alpha = c.swiglu_alpha;
     p.limit = c.swiglu_limit;
     if (stages & kStageGateUp) {
         p.act = (const uint16_t*)x;
+        p.act_rows = batch;
         p.blocks = (const uint8_t*)w->gate_up_blocks;
         p.scales = (const uint8_t*)w->gate_up_scales;
         p.bias = (const uint16_t*)w->gate_up_bias;
@@ -154,16 +169,20 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
     }
     if (stages & kStageDown) {
         p.act = ws.h;
+        p.act_rows = N;
         p.blocks = (const uint8_t*)w->down_blocks;
         p.scales = (const uint8_t*)w->down_scales;
         p.bias = (const uint16_t*)w->down_bias;
         p.out = ws.y;
         p.Kdim = c.intermediate;
         p.R = c.hidden;
+        p.split = ws.split;
         if ((rc = gemv_launch(kModeDown, p, max_slots, batch, s))) return rc;
     }
     if (stages & kStageCombine) {
-        if ((rc = combine_launch(ws.y, ws.pos, wts, (uint16_t*)out, batch, c.hidden, c.top_k, s))) return rc;
+        if ((rc = combine_launch(ws.y, ws.split, (size_t)N * c.hidden, ws.pos, wts, (uint16_t*)out, batch, c.hidden,
+                                 c.top_k, s)))
+            return rc;
     }
     return ok();
 }

@@ -9,18 +9,18 @@
 // below any realistic top-k gap, so this kernel's indices equal the CPU oracle's
 // serial sums bit for bit.
 //
-// Layout: one workgroup of 4 waves handles TB tokens. Wave w computes experts
-// w, w+4, ... : each lane accumulates 8-element chunks (16-byte loads, so a wave
-// reads one contiguous 1 KiB slice of the expert row per step) and a butterfly
-// reduction finishes the dot. Logits go to LDS; then one wave per token runs the
-// selection with a wave-wide arg-max per round.
+// Layout: one workgroup of 8 waves handles TB tokens. Wave w computes experts
+// w*EPI.., with every lane's 16-byte chunks of all EPI router rows and TB token
+// rows loaded up front (a wave reads contiguous 1 KiB slices of each row), then a
+// butterfly reduction per dot. Logits go to LDS; then one wave per token runs
+// the selection with a wave-wide arg-max per round.
 #include "common.h"
 #include "capi_internal.h"
 #include "experts.h"
 
 namespace physllm {
 
-constexpr int kRouterThreads = 256;
+constexpr int kRouterThreads = 512;  // 8 waves
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;
 
@@ -34,64 +34,108 @@ __device__ __forceinline__ bool rank_beats(double av, int ae, double bv, int be)
     return ae < be;
 }
 
-template <int TB>
+__device__ __forceinline__ void bf16x8_to_f64(uint4 v, double (&d)[8]) {
+    d[0] = (double)bf16_lo(v.x);
+    d[1] = (double)bf16_hi(v.x);
+    d[2] = (double)bf16_lo(v.y);
+    d[3] = (double)bf16_hi(v.y);
+    d[4] = (double)bf16_lo(v.z);
+    d[5] = (double)bf16_hi(v.z);
+    d[6] = (double)bf16_lo(v.w);
+    d[7] = (double)bf16_hi(v.w);
+}
+
+// Logits of TB tokens x EPI experts for one wave: each lane owns 8-element chunks
+// c = lane + 64 u; all U chunks of every operand are loaded before any is used, so
+// a wave has (EPI + TB) * U 16-byte loads in flight instead of one round trip per
+// chunk. bf16 products are exact in fp64 and summed in fp64.
+template <int TB, int EPI, int U>
+__device__ __forceinline__ void router_dots(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int t0,
+                                            int ntb, int e0, int E, int H, int lane, double (&acc)[EPI][TB]) {
+#pragma unroll
+    for (int ei = 0; ei < EPI; ++ei)
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) acc[ei][tb] = 0.0;
+    const int nch = H >> 3;
+    for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+        uint4 wv[EPI][U], xv[TB][U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + 64 * u;
+#pragma unroll
+            for (int ei = 0; ei < EPI; ++ei)
+                wv[ei][u] = (c < nch && e0 + ei < E) ? ((const uint4*)(w + (size_t)(e0 + ei) * H))[c]
+                                                     : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb)
+                xv[tb][u] = (c < nch && tb < ntb) ? ((const uint4*)(x + (size_t)(t0 + tb) * H))[c]
+                                                  : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            double xd[TB][8];
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) bf16x8_to_f64(xv[tb][u], xd[tb]);
+#pragma unroll
+            for (int ei = 0; ei < EPI; ++ei) {
+                double wd[8];
+                bf16x8_to_f64(wv[ei][u], wd);
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[ei][tb] = __builtin_fma(xd[tb][i], wd[i], acc[ei][tb]);
+            }
+        }
+    }
+}
+
+template <int TB, int EPI, int U>
 __global__ __launch_bounds__(kRouterThreads) void k_router(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ w,
                                                            const uint16_t* __restrict__ bias, int B, int H,
                                                            int E, int K, int32_t* __restrict__ idx,
                                                            float* __restrict__ wts, int vec) {
     extern __shared__ double lg[];  // [TB][E]
+    constexpr int NW = kRouterThreads / 64;
     const int t0 = blockIdx.x * TB;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int ntb = min(TB, B - t0);
 
-    for (int e = wave; e < E; e += kRouterThreads / 64) {
-        double acc[TB];
-#pragma unroll
-        for (int tb = 0; tb < TB; ++tb) acc[tb] = 0.0;
-        const uint16_t* wr = w + (size_t)e * H;
+    for (int e0 = wave * EPI; e0 < E; e0 += NW * EPI) {
+        double acc[EPI][TB];
         if (vec) {
-            const int nch = H >> 3;
-            for (int c = lane; c < nch; c += 64) {
-                const uint4 wv = ((const uint4*)wr)[c];
-                const uint32_t wa[4] = {wv.x, wv.y, wv.z, wv.w};
-                double wd[8];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    wd[2 * j] = (double)bf16_lo(wa[j]);
-                    wd[2 * j + 1] = (double)bf16_hi(wa[j]);
-                }
-#pragma unroll
-                for (int tb = 0; tb < TB; ++tb) {
-                    if (tb < ntb) {
-                        const uint4 xv = ((const uint4*)(x + (size_t)(t0 + tb) * H))[c];
-                        const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            acc[tb] = __builtin_fma((double)bf16_lo(xa[j]), wd[2 * j], acc[tb]);
-                            acc[tb] = __builtin_fma((double)bf16_hi(xa[j]), wd[2 * j + 1], acc[tb]);
-                        }
-                    }
-                }
-            }
+            router_dots<TB, EPI, U>(x, w, t0, ntb, e0, E, H, lane, acc);
         } else {
-            for (int d = lane; d < H; d += 64) {
-                const double wv = (double)bf16_to_f32(wr[d]);
 #pragma unroll
-                for (int tb = 0; tb < TB; ++tb)
-                    if (tb < ntb) acc[tb] = __builtin_fma((double)bf16_to_f32(x[(size_t)(t0 + tb) * H + d]), wv, acc[tb]);
+            for (int ei = 0; ei < EPI; ++ei)
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb) acc[ei][tb] = 0.0;
+            for (int d = lane; d < H; d += 64) {
+#pragma unroll
+                for (int ei = 0; ei < EPI; ++ei) {
+                    if (e0 + ei >= E) continue;
+                    const double wv = (double)bf16_to_f32(w[(size_t)(e0 + ei) * H + d]);
+#pragma unroll
+                    for (int tb = 0; tb < TB; ++tb)
+                        if (tb < ntb)
+                            acc[ei][tb] = __builtin_fma((double)bf16_to_f32(x[(size_t)(t0 + tb) * H + d]), wv, acc[ei][tb]);
+                }
             }
         }
-        const double b = bias ? (double)bf16_to_f32(bias[e]) : 0.0;
 #pragma unroll
-        for (int tb = 0; tb < TB; ++tb) {
-            const double s = wave_sum_f64(acc[tb]);
-            if (lane == 0) lg[tb * E + e] = s + b;
+        for (int ei = 0; ei < EPI; ++ei) {
+            const int e = e0 + ei;
+            const double b = (bias && e < E) ? (double)bf16_to_f32(bias[e]) : 0.0;
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+                const double sum = wave_sum_f64(acc[ei][tb]);
+                if (lane == 0 && e < E) lg[tb * E + e] = sum + b;
+            }
         }
     }
     __syncthreads();
 
-    for (int tb = wave; tb < ntb; tb += kRouterThreads / 64) {
+    for (int tb = wave; tb < ntb; tb += NW) {
         const int t = t0 + tb;
         const double* L = lg + tb * E;
         uint32_t used = 0;  // bit i: expert lane + 64 i taken
@@ -136,13 +180,15 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
     if (B == 0) return ok();
     if (!x || !w || !idx || !wts) return set_error(PHYSLLM_MOE_EINVAL, "router: null pointer");
     const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0);
-    if (B >= 64) {
+    if (B > 1024) {
+        // prefill: 4 tokens per group share every loaded router row
         constexpr int TB = 4;
-        hipLaunchKernelGGL(k_router<TB>, dim3((B + TB - 1) / TB), dim3(kRouterThreads),
+        hipLaunchKernelGGL((k_router<TB, 1, 4>), dim3((B + TB - 1) / TB), dim3(kRouterThreads),
                            (size_t)TB * E * sizeof(double), stream, (const uint16_t*)x, (const uint16_t*)w,
                            (const uint16_t*)bias, B, H, E, K, (int32_t*)idx, (float*)wts, vec);
     } else {
-        hipLaunchKernelGGL(k_router<1>, dim3(B), dim3(kRouterThreads), (size_t)E * sizeof(double), stream,
+        // decode: one token per group, 4 experts' rows in flight per wave
+        hipLaunchKernelGGL((k_router<1, 4, 6>), dim3(B), dim3(kRouterThreads), (size_t)E * sizeof(double), stream,
                            (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, B, H, E, K,
                            (int32_t*)idx, (float*)wts, vec);
     }
@@ -158,7 +204,9 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
 //      wave comes from a ballot-based match, the wave's base from per-wave counts
 //      of the chunk; running per-expert totals carry across chunks.
 // Outputs perm (sorted position -> pair id), pos (pair id -> sorted position),
-// counts, offsets, active[n_active] (touched experts, ascending) and n_active.
+// counts, offsets and the work-slot table slots[E]: slot a < #touched holds
+// {expert, tokens, first sorted position, 0} for the a-th touched expert
+// (ascending id), later slots hold zeros.
 // Pairs whose expert id is outside [0, E) are dropped.
 // ---------------------------------------------------------------------------
 constexpr int kBucketThreads = 1024;
@@ -184,8 +232,7 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
                                                            int32_t* __restrict__ counts,
                                                            int32_t* __restrict__ offsets,
                                                            int32_t* __restrict__ perm, int32_t* __restrict__ pos,
-                                                           int32_t* __restrict__ active,
-                                                           int32_t* __restrict__ n_active) {
+                                                           int4* __restrict__ slots, int32_t* __restrict__ n_slots) {
     extern __shared__ int smem[];
     int* cnt = smem;                   // [E]
     int* off = cnt + E;                // [E]
@@ -213,11 +260,14 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
             off[tid] = ex;
             counts[tid] = c;
             offsets[tid] = ex;
-            if (active && c > 0) active[na] = tid;
-            if (tid == E - 1) {
-                offsets[E] = ex + c;
-                if (n_active) *n_active = na + (c > 0 ? 1 : 0);
-            }
+            if (tid == E - 1) offsets[E] = ex + c;
+        }
+        if (slots) {
+            // touched experts take slots 0..#touched-1; the rest are cleared
+            const int ntouched = __syncthreads_count(tid < E && c > 0);
+            if (tid == 0 && n_slots) *n_slots = ntouched;
+            if (tid < E && c > 0) slots[na] = make_int4(tid, c, ex, 0);
+            if (tid >= ntouched && tid < E) slots[tid] = make_int4(0, 0, 0, 0);
         }
     }
     __syncthreads();
@@ -257,8 +307,8 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
 
 size_t bucket_smem_bytes(int E) { return sizeof(int) * ((size_t)3 * E + kBucketThreads + 16 * (size_t)E); }
 
-int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, void* perm, void* pos, void* active,
-                  void* n_active, hipStream_t stream) {
+int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, void* perm, void* pos, void* slots,
+                  void* n_slots, hipStream_t stream) {
     static bool attr_set = false;
     const size_t smem = bucket_smem_bytes(E);
     if (!attr_set) {
@@ -267,8 +317,8 @@ int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, vo
         attr_set = true;
     }
     hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBucketThreads), smem, stream, (const int32_t*)idx, N, E,
-                       (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm, (int32_t*)pos, (int32_t*)active,
-                       (int32_t*)n_active);
+                       (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm, (int32_t*)pos, (int4*)slots,
+                       (int32_t*)n_slots);
     return check_launch("bucket");
 }
 

@@ -27,6 +27,19 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "MoE-layer tokens/sec + % HBM peak (decode) / % MFMA peak (prefill), 1 GPU"
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+
+
+def measured_traffic(cfg_index: int):
+    """HBM bytes per launch of the gate_up kernel from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration)."""
+    import re
+    try:
+        text = open(TRAFFIC_SUMMARY).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic\[config%d\.gate_up\]\s*=\s*(\d+)" % cfg_index, text, re.M)
+    return int(m.group(1)) if m else None
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 
@@ -43,6 +56,11 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=[0, 2, 3, 4])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 512 MiB device-to-device copy three times (the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
+    ap.add_argument("--graph", action="store_true",
+                    help="time HIP-graph replays of the layer instead of eager C-ABI calls")
     return ap.parse_args()
 
 
@@ -56,6 +74,16 @@ def main():
 
     import torch
 
+    if args.calibrate_copy:
+        n = 512 * 1024 * 1024
+        a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "launches": 3}))
+        return
+
     from physllm_amd import ops
     from physllm_amd import synthetic as syn
 
@@ -66,18 +94,31 @@ def main():
     B, H, I, E, K = x.shape[0], layer.hidden, layer.intermediate, layer.num_experts, layer.top_k
 
     dl0 = ops.DeviceMoELayer.from_host(layer)
+    xd = torch.from_numpy(x.view(np.int16)).cuda()
+    stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
+
+    # touched experts (the device router; routing is deterministic)
+    idx = torch.empty((B, K), dtype=torch.int32, device="cuda")
+    wt = torch.empty((B, K), dtype=torch.float32, device="cuda")
+    ops.route_topk(xd, dl0.tensors["router_w"], dl0.tensors["router_b"], idx, wt, K, s)
+    torch.cuda.synchronize()
+    counts = np.bincount(idx.cpu().numpy().reshape(-1), minlength=E)
+    e_touched = int((counts > 0).sum())
+    layer_bytes = e_touched * layer.expert_bytes + E * H * 2 + E * 2 + B * H * 2 * 2
+
+    # Steps rotate over device copies of the weights so that the bytes a step touches,
+    # times the copies, exceed 1 GB: the 256 MB Infinity Cache cannot serve them.
     copies = [dl0]
-    n_copies = 1 if cfg_i == 3 else max(1, math.ceil(1.1e9 / layer.weight_bytes))
+    n_copies = 1 if cfg_i == 3 else max(1, math.ceil(1.1e9 / layer_bytes))
     for _ in range(n_copies - 1):
         t = {k: (v.clone() if v is not None else None) for k, v in dl0.tensors.items()}
         copies.append(ops.DeviceMoELayer.from_tensors(H, I, E, K, t, layer.alpha, layer.limit))
-    log(f"[bench] {n_copies} weight copies x {layer.weight_bytes / 1e6:.1f} MB")
+    log(f"[bench] {e_touched} experts touched ({layer_bytes / 1e6:.1f} MB/step); "
+        f"{n_copies} weight copies x {layer.weight_bytes / 1e6:.1f} MB")
 
-    xd = torch.from_numpy(x.view(np.int16)).cuda()
     out = torch.empty((B, H), dtype=torch.int16, device="cuda")
     ws = torch.empty(dl0.workspace_bytes(B), dtype=torch.uint8, device="cuda")
-    stream = torch.cuda.current_stream()
-    s = stream.cuda_stream
 
     def step(i):
         copies[i % n_copies].forward(xd, out, ws, stream=s)
@@ -85,49 +126,77 @@ def main():
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    ref_out = out.clone()
 
-    # ---- timed region: K whole-layer steps ------------------------------------------
+    # eager: one C-ABI call per step from the host
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
     ev0.record(stream)
     for i in range(args.steps):
         step(i)
     ev1.record(stream)
     torch.cuda.synchronize()
+    eager_ms = ev0.elapsed_time(ev1) / args.steps
+
+    # graph: each weight copy's layer captured once (the layer has no host sync and
+    # records no memset), then replayed; this is how a serving loop runs the layer
+    graphs = []
+    if args.graph:
+        for c in range(n_copies):
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph):
+                copies[c].forward(xd, out, ws)
+            graphs.append(gph)
+        for i in range(max(args.warmup, n_copies)):
+            graphs[i % n_copies].replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_out), "graph replay output differs from the eager output"
+
+    # ---- timed region: K whole-layer steps ------------------------------------------
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        if graphs:
+            graphs[i % n_copies].replay()
+        else:
+            step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    if graphs:
+        assert torch.equal(out, ref_out), "timed replays changed the output"
 
-    # ---- per-stage timing (events between the stage entry points, same stream) -------
+    # ---- per-stage timing: each stage entry point launched K times back to back
+    # (rotating weight copies) between two events on the launch stream; the stages
+    # are idempotent given the routing state the route stage left in the workspace.
     from physllm_amd.capi import check, lib
     import ctypes
     L = lib()
     nbytes = ws.numel()
-    stage_ms = np.zeros(4)
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
-    for i in range(args.steps):
-        d = copies[i % n_copies]
-        c, w = ctypes.byref(d.cfg), ctypes.byref(d.weights)
-        evs[0].record(stream)
-        check(L.physllm_moe_stage_route(c, w, xd.data_ptr(), B, None, None, ws.data_ptr(), nbytes, s))
-        evs[1].record(stream)
-        check(L.physllm_moe_stage_gate_up(c, w, xd.data_ptr(), B, ws.data_ptr(), nbytes, s))
-        evs[2].record(stream)
-        check(L.physllm_moe_stage_down(c, w, B, ws.data_ptr(), nbytes, s))
-        evs[3].record(stream)
-        check(L.physllm_moe_stage_combine(c, B, out.data_ptr(), None, ws.data_ptr(), nbytes, s))
-        evs[4].record(stream)
-        torch.cuda.synchronize()
-        stage_ms += [evs[j].elapsed_time(evs[j + 1]) for j in range(4)]
-    stage_ms /= args.steps
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
 
-    # touched experts (routing is deterministic; read once, outside the timed region)
-    idx = torch.empty((B, K), dtype=torch.int32, device="cuda")
-    wt = torch.empty((B, K), dtype=torch.float32, device="cuda")
-    ops.route_topk(xd, dl0.tensors["router_w"], dl0.tensors["router_b"], idx, wt, K, s)
-    torch.cuda.synchronize()
-    counts = np.bincount(idx.cpu().numpy().reshape(-1), minlength=E)
-    e_touched = int((counts > 0).sum())
+    def cw(i):
+        d = copies[i % n_copies]
+        return ctypes.byref(d.cfg), ctypes.byref(d.weights)
+
+    stage_calls = [
+        lambda i: L.physllm_moe_stage_route(*cw(i), xd.data_ptr(), B, None, None, ws.data_ptr(), nbytes, s),
+        lambda i: L.physllm_moe_stage_gate_up(*cw(i), xd.data_ptr(), B, ws.data_ptr(), nbytes, s),
+        lambda i: L.physllm_moe_stage_down(*cw(i), B, ws.data_ptr(), nbytes, s),
+        lambda i: L.physllm_moe_stage_combine(cw(i)[0], B, out.data_ptr(), None, ws.data_ptr(), nbytes, s),
+    ]
+    stage_ms = np.zeros(4)
+    for j, call in enumerate(stage_calls):
+        check(call(0))
+        torch.cuda.synchronize()
+        evs[0].record(stream)
+        for i in range(args.steps):
+            check(call(i))
+        evs[1].record(stream)
+        torch.cuda.synchronize()
+        stage_ms[j] = evs[0].elapsed_time(evs[1]) / args.steps
+    assert torch.equal(out, ref_out), "staged entry points disagree with the layer entry point"
 
     # ---- roofline of the dominant kernel (gate_up) ---------------------------------------
     gu_expert_bytes = (2 * I * H // 2) + (2 * I * H // 32) + 2 * (2 * I)
@@ -136,15 +205,15 @@ def main():
         flops = 2.0 * B * K * (2 * I) * H
         achieved = flops / (gate_up_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_MFMA_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                "kernel": "gate_up grouped GEMM", "work_per_launch": flops}
+                "unit": "TFLOP/s", "frac": round(achieved / BF16_MFMA_PEAK_TFLOPS, 4),
+                "traffic": measured_traffic(cfg_i),
+                "kernel": "gate_up grouped GEMM (k_mx_gemm<0>)", "work_per_launch": flops}
     else:
         alg = e_touched * gu_expert_bytes + B * H * 2 + B * K * I * 2
         achieved = alg / (gate_up_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "gate_up grouped GEMV (k_mx_gemv<0>)", "work_per_launch": alg}
-    layer_bytes = e_touched * layer.expert_bytes + E * H * 2 + E * 2 + B * H * 2 * 2
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(cfg_i),
+                "kernel": "gate_up grouped GEMV (k_mx_gemv<0,NS>)", "work_per_launch": alg}
 
     # ---- CPU baseline (oracle on this host's cores, bounded sample) ----------------------
     cpu = None
@@ -185,7 +254,9 @@ def main():
                   "hbm_frac": round(layer_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                   "stage_ms": {"route": round(stage_ms[0], 5), "gate_up": round(stage_ms[1], 5),
                                "down": round(stage_ms[2], 5), "combine": round(stage_ms[3], 5)},
-                  "wall_s_timed_region": round(wall, 4)},
+                  "wall_s_timed_region": round(wall, 4),
+                  "launch": "hip graph replay" if args.graph else "eager C-ABI call per step",
+                  "eager_ms_per_step": round(eager_ms, 5)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)

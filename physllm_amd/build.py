@@ -68,5 +68,23 @@ def build(verbose: bool = True) -> str:
     return LIB_PATH
 
 
+def build_host_test(verbose: bool = True) -> str:
+    """C++ host-layer test driver (tests/cpp/test_host_api), linked against the
+    library and the CPU oracle (oracle/liboracle.so must be built first)."""
+    root = os.path.dirname(HERE)
+    src = os.path.join(root, "tests", "cpp", "test_host_api.cpp")
+    out = os.path.join(root, "tests", "cpp", "test_host_api")
+    cmd = [hipcc(), "-O2", "-std=c++17", src, "-o", out,
+           "-L" + HERE, "-lphysllm_moe", "-L" + os.path.join(root, "oracle"), "-loracle",
+           "-Wl,-rpath," + HERE, "-Wl,-rpath," + os.path.join(root, "oracle"),
+           "-Wl,-rpath,$ORIGIN/../../physllm_amd", "-Wl,-rpath,$ORIGIN/../../oracle"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host test build failed:\n{r.stdout}\n{r.stderr}")
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
 if __name__ == "__main__":
     build()

@@ -36,6 +36,11 @@ int gemv_launch(int mode, const GemvParams& p, int max_slots, int max_tokens, hi
 int combine_launch(const float* y, int nsplit, size_t split_stride, const int32_t* pos, const float* wts,
                    uint16_t* out, int B, int H, int K, hipStream_t stream);
 int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, void* perm, void* pos, void* slots,
-                  void* n_slots, hipStream_t stream);
+                  void* n_slots, void* tprefix, int tile_n, hipStream_t stream);
+// Grouped GEMM for many tokens per expert; tprefix = per-slot exclusive prefix of
+// kGemmTileN-token tiles (from bucketing).
+constexpr int kGemmTileN = 128;
+int gemm_launch(int mode, const GemvParams& p, const int32_t* tprefix, int max_slots, int n_pairs,
+                hipStream_t stream);
 
 }  // namespace physllm

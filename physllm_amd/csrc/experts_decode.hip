@@ -252,7 +252,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p) {
     const uint32_t woff = (uint32_t)(r0 + m) * row_bytes + (uint32_t)(kb0 + g) * 16u;
     u32x4_t wq[kGemvNit];
 #pragma unroll
-    for (int j = 0; j < kGemvNit; ++j) wq[j] = buf_load16(rw, woff, 64 * j);
+    for (int j = 0; j < kGemvNit; ++j)  // only the k-steps of this split's K range
+        wq[j] = (4 * j < nblk) ? buf_load16(rw, woff, 64 * j) : u32x4_t{0u, 0u, 0u, 0u};
     const uint32_t soff = (uint32_t)r0 * NB + lane * 16u;  // 16 rows x NB bytes, contiguous
     const u32x4_t sv0 = buf_load16(rs, soff, 0);
     const u32x4_t sv1 = buf_load16(rs, soff, 1024);

@@ -1,0 +1,232 @@
+// Prefill-regime expert kernels for gfx950: grouped MXFP4 x bf16 GEMM on MFMA.
+//
+// With hundreds of tokens per expert the expert projections are GEMMs
+// (2 * tokens * rows * K flops against rows * K / 2 code bytes): MFMA-bound. One
+// workgroup (4 waves, 2 x 2) computes a 128-row x 128-token tile of one expert:
+//   A = weights, MXFP4: each wave keeps its 64 rows' stripes of the current
+//       k-step in registers (one 16-byte buffer load per lane per 16-row tile =
+//       one full MX block of one row) and decodes them with
+//       v_cvt_scalef32_pk_bf16_fp4 right before the MFMA;
+//   B = activations, bf16: the tile's 128 token rows (gathered through the
+//       bucketing permutation for gate_up, contiguous for down) are staged in
+//       LDS, double-buffered across k-steps, rows padded by 16 bytes so the 16
+//       token columns of a fragment read hit distinct banks.
+// A k-step covers 4 MX blocks (128 elements); lane group g supplies block g of
+// the step to both operands (the same K-permutation on A and B), so one MFMA
+// (v_mfma_f32_16x16x32_bf16) consumes 8 elements of each of 4 blocks.
+// Epilogues: gate_up adds the bias and applies the clamped SwiGLU to each lane's
+// (gate, up) row pairs (rows are interleaved) -> h bf16; down adds the bias ->
+// y fp32. Tiles are scheduled from a device-side per-expert prefix of token
+// tiles, and consecutive token tiles of one weight row tile are mapped to the
+// same XCD so they share its L2.
+#include "common.h"
+#include "capi_internal.h"
+#include "experts.h"
+
+namespace physllm {
+
+constexpr int kGemmThreads = 256;
+constexpr int kTM = 128;          // weight rows per tile
+constexpr int kTN = 128;          // tokens per tile
+constexpr int kKS = 128;          // elements per k-step (4 MX blocks)
+constexpr int kBRowU = kKS * 2 / 16 + 1;  // LDS row stride of the B tile in 16-byte units (16 + pad)
+constexpr int kBUnitsPerThread = kTN * (kKS * 2 / 16) / kGemmThreads;  // 8
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4_t gemm_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kGemmThreads, 2) void k_mx_gemm(GemvParams p, const int32_t* __restrict__ tprefix) {
+    extern __shared__ uint4 lds[];
+    // ---- tile id -> (expert slot, row tile, token tile), XCD-aware ----
+    const int G = gridDim.x;  // a multiple of 8
+    const int bid = blockIdx.x;
+    const int t = (bid & 7) * (G >> 3) + (bid >> 3);
+    const int n_slots = *p.n_slots;
+    const int row_tiles = (p.R + kTM - 1) / kTM;
+    if (t >= row_tiles * tprefix[n_slots]) return;
+    int lo = 0, hi = n_slots;  // largest s with row_tiles * tprefix[s] <= t
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (row_tiles * tprefix[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int slot = lo;
+    const int4 si = p.slots[slot];
+    const int e = si.x, ne = si.y, p0 = si.z;
+    const int ntt = (ne + kTN - 1) / kTN;
+    const int local = t - row_tiles * tprefix[slot];
+    const int rtile = local / ntt;
+    const int ttile = local - rtile * ntt;
+    const int row0 = rtile * kTM;
+    const int tok0 = ttile * kTN;
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int m = lane & 15, g = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;  // wave quadrant: rows 64*wm.., tokens 64*wn..
+    const int NB = p.Kdim >> 5;
+    const int nks = (NB + 3) >> 2;
+    const uint32_t row_bytes = (uint32_t)(p.Kdim >> 1);
+    const uint32_t exp_w = (uint32_t)p.R * row_bytes;
+    const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;
+    const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(p.blocks + (size_t)e * exp_w, exp_w);
+    const uint8_t* sbase = p.scales + (size_t)e * exp_s;
+    const __amdgpu_buffer_rsrc_t ract = gemm_rsrc(p.act, (uint32_t)p.act_rows * (uint32_t)p.Kdim * 2u);
+
+    // A: this lane's rows (4 tiles of 16) and its block within each k-step
+    uint32_t aoff[4];
+    int arow[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        arow[mt] = row0 + wm * 64 + mt * 16 + m;
+        aoff[mt] = (uint32_t)arow[mt] * row_bytes + (uint32_t)g * 16u;
+    }
+    // B: this thread's staging units: token rows r = tid/16 + 16u (u < 8), chunk c = tid%16
+    const int bc = threadIdx.x & 15;
+    uint32_t boff[kBUnitsPerThread];
+#pragma unroll
+    for (int u = 0; u < kBUnitsPerThread; ++u) {
+        const int r = (threadIdx.x >> 4) + 16 * u;
+        const int q = min(tok0 + r, ne - 1);  // rows past the expert's tokens: any valid row
+        const uint32_t arow_act = (MODE == kModeGateUp) ? (uint32_t)(p.perm[p0 + q] / p.top_k) : (uint32_t)(p0 + q);
+        boff[u] = arow_act * (uint32_t)(p.Kdim * 2) + (uint32_t)bc * 16u;
+    }
+
+    u32x4_t aq[4];
+    uint32_t as[4];
+    u32x4_t bv[kBUnitsPerThread];
+    auto load_step = [&](int ks) {
+        const int blk = ks * 4 + g;
+        const bool in = blk < NB;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            aq[mt] = gemm_load16(rw, aoff[mt] + (uint32_t)ks * 64u);
+            as[mt] = (in && arow[mt] < p.R) ? (uint32_t)sbase[(size_t)arow[mt] * NB + blk] : 0u;
+        }
+        const int kel = ks * kKS + bc * 8;  // first element of this thread's B chunk
+#pragma unroll
+        for (int u = 0; u < kBUnitsPerThread; ++u)
+            bv[u] = kel < p.Kdim ? gemm_load16(ract, boff[u] + (uint32_t)ks * (kKS * 2)) : u32x4_t{0u, 0u, 0u, 0u};
+    };
+    auto store_b = [&](int buf) {
+        u32x4_t* bs = (u32x4_t*)lds + buf * (kTN * kBRowU);
+#pragma unroll
+        for (int u = 0; u < kBUnitsPerThread; ++u) {
+            const int r = (threadIdx.x >> 4) + 16 * u;
+            bs[r * kBRowU + bc] = bv[u];
+        }
+    };
+
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    load_step(0);
+    store_b(0);
+    __syncthreads();
+    for (int ks = 0; ks < nks; ++ks) {
+        // this step's A (registers) and scales; the next step's loads go out first
+        u32x4_t a_cur[4];
+        uint32_t s_cur[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            a_cur[mt] = aq[mt];
+            s_cur[mt] = as[mt];
+        }
+        const bool more = ks + 1 < nks;
+        if (more) load_step(ks + 1);
+        const bool in = ks * 4 + g < NB;
+        const uint4* bs = lds + (ks & 1) * (kTN * kBRowU);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // B fragments: token column m of each 16-token tile, 8 elements of block g
+            uint4 b[4];
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) {
+                const int r = wn * 64 + nt * 16 + m;
+                const uint4* src = bs + r * kBRowU + g * 4 + i;
+                b[nt] = *src;
+            }
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const uint32_t code = in ? a_cur[mt][i] : 0u;
+                const bf16x8_t a = mx_cvt8(code, e8m0_scale_operand(s_cur[mt]));
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = mfma16x16x32(a, as_bf16x8(b[nt]), acc[mt][nt]);
+            }
+        }
+        if (more) {
+            store_b((ks + 1) & 1);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue ----
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        const int q = tok0 + wn * 64 + nt * 16 + m;  // token column of this lane
+        if (q >= ne) continue;
+        const int pp = p0 + q;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const int rr = row0 + wm * 64 + mt * 16 + 4 * g;
+            if (rr >= p.R) continue;
+            float bsum[4] = {0.f, 0.f, 0.f, 0.f};
+            if (p.bias) {
+                const uint2 bb = *(const uint2*)(p.bias + (size_t)e * p.R + rr);
+                bsum[0] = bf16_lo(bb.x);
+                bsum[1] = bf16_hi(bb.x);
+                bsum[2] = bf16_lo(bb.y);
+                bsum[3] = bf16_hi(bb.y);
+            }
+            const f32x4_t c = acc[mt][nt];
+            if (MODE == kModeGateUp) {
+                const float h0 = swiglu(c[0] + bsum[0], c[1] + bsum[1], p.alpha, p.limit);
+                const float h1 = swiglu(c[2] + bsum[2], c[3] + bsum[3], p.alpha, p.limit);
+                const int I = p.R >> 1;
+                uint32_t* hout = (uint32_t*)((uint16_t*)p.out + (size_t)pp * I + (rr >> 1));
+                *hout = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
+            } else {
+                float4 y;
+                y.x = c[0] + bsum[0];
+                y.y = c[1] + bsum[1];
+                y.z = c[2] + bsum[2];
+                y.w = c[3] + bsum[3];
+                *(float4*)((float*)p.out + (size_t)pp * p.R + rr) = y;
+            }
+        }
+    }
+}
+
+int gemm_launch(int mode, const GemvParams& p, const int32_t* tprefix, int max_slots, int n_pairs,
+                hipStream_t stream) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void*)k_mx_gemm<kModeGateUp>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024);
+        (void)hipFuncSetAttribute((const void*)k_mx_gemm<kModeDown>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024);
+        attr_set = true;
+    }
+    if (p.split != 1) return set_error(PHYSLLM_MOE_EINVAL, "gemm: split must be 1");
+    const int row_tiles = (p.R + kTM - 1) / kTM;
+    // upper bound on token tiles: every touched expert may add one partial tile
+    const long token_tiles = (long)(n_pairs + kTN - 1) / kTN + max_slots;
+    long tiles = row_tiles * token_tiles;
+    tiles = (tiles + 7) & ~7L;
+    if (tiles > 0x7fffffffL) return set_error(PHYSLLM_MOE_EINVAL, "gemm: too many tiles");
+    const size_t lds = (size_t)2 * kTN * kBRowU * 16;
+    if (mode == kModeGateUp)
+        hipLaunchKernelGGL(k_mx_gemm<kModeGateUp>, dim3((unsigned)tiles), dim3(kGemmThreads), lds, stream, p, tprefix);
+    else
+        hipLaunchKernelGGL(k_mx_gemm<kModeDown>, dim3((unsigned)tiles), dim3(kGemmThreads), lds, stream, p, tprefix);
+    return check_launch(mode == kModeGateUp ? "gate_up gemm" : "down gemm");
+}
+
+}  // namespace physllm

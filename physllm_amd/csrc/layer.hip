@@ -45,6 +45,7 @@ struct Workspace {
     int32_t* offsets;
     int4* slots;
     int32_t* n_slots;
+    int32_t* tprefix;  // [E+1] token-tile prefix over slots
     int32_t* perm;
     int32_t* pos;
     uint16_t* h;
@@ -55,9 +56,17 @@ struct Workspace {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Many tokens per touched expert (prefill): grouped GEMM; otherwise the GEMV.
+static bool use_gemm(const physllm_moe_config& c, int B) {
+    const int64_t N = (int64_t)B * c.top_k;
+    const int64_t slots = std::min<int64_t>(N, c.num_experts);
+    return N >= 64 * slots;
+}
+
 // K splits of the down projection: enough 16-row work tiles (one per wave) to
 // cover the chip when few experts are touched (decode at small batch).
 static int down_split(const physllm_moe_config& c, int B) {
+    if (use_gemm(c, B)) return 1;
     const int64_t slots = std::min<int64_t>((int64_t)B * c.top_k, c.num_experts);
     const int64_t tiles = slots * ((c.hidden + 15) / 16);
     const int64_t want = 2048;
@@ -82,6 +91,7 @@ static Workspace carve(const physllm_moe_config& c, int B, char* base) {
     w.offsets = (int32_t*)take((E + 1) * 4);
     w.slots = (int4*)take(E * 16);
     w.n_slots = (int32_t*)take(4);
+    w.tprefix = (int32_t*)take((E + 1) * 4);
     w.perm = (int32_t*)take(N * 4);
     w.pos = (int32_t*)take(N * 4);
     w.h = (uint16_t*)take(N * (size_t)c.intermediate * 2);
@@ -143,7 +153,8 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
     if (stages & kStageRoute) {
         if ((rc = router_launch(x, w->router_w, w->router_b, batch, c.hidden, c.num_experts, c.top_k, idx, wts, s)))
             return rc;
-        if ((rc = bucket_launch(idx, N, c.num_experts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.slots, ws.n_slots, s)))
+        if ((rc = bucket_launch(idx, N, c.num_experts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.slots, ws.n_slots,
+                                ws.tprefix, kGemmTileN, s)))
             return rc;
     }
     const int max_slots = N < c.num_experts ? N : c.num_experts;
@@ -165,7 +176,9 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
         p.out = ws.h;
         p.Kdim = c.hidden;
         p.R = 2 * c.intermediate;
-        if ((rc = gemv_launch(kModeGateUp, p, max_slots, batch, s))) return rc;
+        rc = use_gemm(c, batch) ? gemm_launch(kModeGateUp, p, ws.tprefix, max_slots, N, s)
+                                : gemv_launch(kModeGateUp, p, max_slots, batch, s);
+        if (rc) return rc;
     }
     if (stages & kStageDown) {
         p.act = ws.h;
@@ -177,7 +190,9 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
         p.Kdim = c.intermediate;
         p.R = c.hidden;
         p.split = ws.split;
-        if ((rc = gemv_launch(kModeDown, p, max_slots, batch, s))) return rc;
+        rc = use_gemm(c, batch) ? gemm_launch(kModeDown, p, ws.tprefix, max_slots, N, s)
+                                : gemv_launch(kModeDown, p, max_slots, batch, s);
+        if (rc) return rc;
     }
     if (stages & kStageCombine) {
         if ((rc = combine_launch(ws.y, ws.split, (size_t)N * c.hidden, ws.pos, wts, (uint16_t*)out, batch, c.hidden,

@@ -232,7 +232,8 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
                                                            int32_t* __restrict__ counts,
                                                            int32_t* __restrict__ offsets,
                                                            int32_t* __restrict__ perm, int32_t* __restrict__ pos,
-                                                           int4* __restrict__ slots, int32_t* __restrict__ n_slots) {
+                                                           int4* __restrict__ slots, int32_t* __restrict__ n_slots,
+                                                           int32_t* __restrict__ tprefix, int tile_n) {
     extern __shared__ int smem[];
     int* cnt = smem;                   // [E]
     int* off = cnt + E;                // [E]
@@ -268,6 +269,13 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
             if (tid == 0 && n_slots) *n_slots = ntouched;
             if (tid < E && c > 0) slots[na] = make_int4(tid, c, ex, 0);
             if (tid >= ntouched && tid < E) slots[tid] = make_int4(0, 0, 0, 0);
+            if (tprefix) {
+                // exclusive prefix of token tiles over the slots (GEMM tile scheduling)
+                const int nt = (c + tile_n - 1) / tile_n;
+                const int tex = block_excl_scan(nt, scan, E);
+                if (tid < E && c > 0) tprefix[na] = tex;
+                if (tid == E - 1) tprefix[ntouched] = tex + nt;
+            }
         }
     }
     __syncthreads();
@@ -308,7 +316,7 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
 size_t bucket_smem_bytes(int E) { return sizeof(int) * ((size_t)3 * E + kBucketThreads + 16 * (size_t)E); }
 
 int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, void* perm, void* pos, void* slots,
-                  void* n_slots, hipStream_t stream) {
+                  void* n_slots, void* tprefix, int tile_n, hipStream_t stream) {
     static bool attr_set = false;
     const size_t smem = bucket_smem_bytes(E);
     if (!attr_set) {
@@ -318,7 +326,7 @@ int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, vo
     }
     hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBucketThreads), smem, stream, (const int32_t*)idx, N, E,
                        (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm, (int32_t*)pos, (int4*)slots,
-                       (int32_t*)n_slots);
+                       (int32_t*)n_slots, (int32_t*)tprefix, tile_n);
     return check_launch("bucket");
 }
 
@@ -338,7 +346,7 @@ extern "C" int physllm_moe_bucket(const void* idx, int batch, int top_k, int num
         return set_error(PHYSLLM_MOE_EINVAL, "bucket: bad sizes");
     if ((int64_t)batch * top_k > 0x7fffffffLL) return set_error(PHYSLLM_MOE_EINVAL, "bucket: batch*top_k too large");
     if (!idx || !counts || !offsets || !perm || !pos) return set_error(PHYSLLM_MOE_EINVAL, "bucket: null pointer");
-    return bucket_launch(idx, batch * top_k, num_experts, counts, offsets, perm, pos, nullptr, nullptr,
+    return bucket_launch(idx, batch * top_k, num_experts, counts, offsets, perm, pos, nullptr, nullptr, nullptr, 1,
                          (hipStream_t)stream);
 }
 

@@ -201,6 +201,17 @@ def test_layer_odd_shapes(oracle, E, H, I, K, B):
     _check_layer(oracle, layer, x, f"E={E} H={H} I={I} K={K} B={B}")
 
 
+@pytest.mark.parametrize("E,H,I,K,B", [(4, 256, 128, 2, 512), (3, 224, 96, 1, 300), (8, 2880, 2880, 4, 1024),
+                                       (2, 160, 160, 2, 700)])
+def test_layer_grouped_gemm_path(oracle, E, H, I, K, B):
+    """Shapes with >= 64 routed tokens per touched expert take the grouped-GEMM
+    (prefill) kernels: partial 128-row tiles (R = 192, 160), partial 128-token
+    tiles, and K ranges that end inside a 128-element step (H = 224, 160)."""
+    layer = syn.make_layer(E, H, I, K, seed=E * 100 + B)
+    x = syn.make_x(B, H, seed=B)
+    _check_layer(oracle, layer, x, f"gemm E={E} H={H} I={I} K={K} B={B}")
+
+
 def test_layer_without_biases(oracle):
     layer = syn.make_layer(8, 128, 64, 2, seed=4, with_bias=False)
     x = syn.make_x(9, 128, seed=4)

@@ -8,6 +8,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 #define PHYSLLM_WAVE 64
 
@@ -80,16 +81,68 @@ __device__ __forceinline__ float swiglu(float g, float u, float alpha, float lim
 }
 
 // ---- wave reductions ----------------------------------------------------------
+// Sums over the 64 lanes without LDS round trips: DPP quad swaps and row
+// mirrors inside each 16-lane row, then the gfx950 cross-row swaps
+// (v_permlane16_swap, v_permlane32_swap). Every lane ends with the same value;
+// the pairing order is fixed, so the result is deterministic.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint32_t lo = __builtin_amdgcn_update_dpp(0u, (uint32_t)__double2loint(v), CTRL, 0xf, 0xf, false);
+    const uint32_t hi = __builtin_amdgcn_update_dpp(0u, (uint32_t)__double2hiint(v), CTRL, 0xf, 0xf, false);
+    return __hiloint2double((int)hi, (int)lo);
+}
+// Pair sums across 16-lane rows: v_permlane16_swap(v, v) returns the rows
+// paired (0,1) and (2,3) in its two results, one from each row of a pair in
+// every lane, so their sum is the pair's sum in every lane (v_permlane32_swap:
+// rows (0,2) and (1,3)); the operands arrive in the same order everywhere.
+__device__ __forceinline__ float rowpair16_sum_f32(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float rowpair32_sum_f32(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ double rowpair16_sum_f64(double v) {
+    const uint32_t lo = (uint32_t)__double2loint(v), hi = (uint32_t)__double2hiint(v);
+    const auto rl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto rh = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    return __hiloint2double((int)rh[0], (int)rl[0]) + __hiloint2double((int)rh[1], (int)rl[1]);
+}
+__device__ __forceinline__ double rowpair32_sum_f64(double v) {
+    const uint32_t lo = (uint32_t)__double2loint(v), hi = (uint32_t)__double2hiint(v);
+    const auto rl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto rh = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    return __hiloint2double((int)rh[0], (int)rl[0]) + __hiloint2double((int)rh[1], (int)rl[1]);
+}
+
+constexpr int kDppXor1 = 0xb1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4e;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within each 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within each 16
+
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    v += dpp_f32<kDppHalfMirror>(v);
+    v += dpp_f32<kDppMirror>(v);
+    v = rowpair16_sum_f32(v);
+    return rowpair32_sum_f32(v);
 }
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_f64<kDppXor1>(v);
+    v += dpp_f64<kDppXor2>(v);
+    v += dpp_f64<kDppHalfMirror>(v);
+    v += dpp_f64<kDppMirror>(v);
+    v = rowpair16_sum_f64(v);
+    return rowpair32_sum_f64(v);
 }
 
 }  // namespace physllm

@@ -19,6 +19,9 @@ struct GemvParams {
     const int32_t* perm;     // [N] sorted position -> pair id
     const int4* slots;       // [E] {expert, tokens, first sorted position, 0}; tokens = 0 past the touched ones
     const int32_t* n_slots;  // [1] number of touched experts
+    const int4* passes;      // [<= N/16 + E] {expert, tokens <= 16, first sorted position, chunk | chunks << 16}:
+                             // each touched expert's tokens in chunks of kPassRows, in slot order (decode only)
+    const int32_t* n_passes; // [1]
     void* out;               // gate_up: h bf16 [N, R/2]; down: y fp32 [N, R] (by sorted position)
     int act_rows;            // rows of act (gate_up: batch; down: N)
     int Kdim;                // reduction length (H for gate_up, I for down)
@@ -31,12 +34,16 @@ struct GemvParams {
 };
 
 constexpr int kMaxSplit = 4;
+constexpr int kPassRows = 16;  // tokens per pass-table entry (the MFMA's N)
 
 int gemv_launch(int mode, const GemvParams& p, int max_slots, int max_tokens, hipStream_t stream);
 int combine_launch(const float* y, int nsplit, size_t split_stride, const int32_t* pos, const float* wts,
                    uint16_t* out, int B, int H, int K, hipStream_t stream);
+// Counting sort of the routed pairs by expert. Optional outputs (nullable): the
+// slot table and its count, the per-slot prefix of tile_n-token tiles, and the
+// pass table (chunks of kPassRows tokens) with its count.
 int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, void* perm, void* pos, void* slots,
-                  void* n_slots, void* tprefix, int tile_n, hipStream_t stream);
+                  void* n_slots, void* tprefix, int tile_n, void* passes, void* n_passes, hipStream_t stream);
 // Grouped GEMM for many tokens per expert; tprefix = per-slot exclusive prefix of
 // kGemmTileN-token tiles (from bucketing).
 constexpr int kGemmTileN = 128;

@@ -370,6 +370,217 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming form (decode with many touched experts). One 8-wave workgroup per
+// CU walks a contiguous range of work items (pass-table entry, K split, 128-row
+// set): at most 16 tokens of one expert against 128 weight rows; wave w owns
+// rows 16w..16w+15 of the set. The 23 weight stripes of a tile sit in a
+// circular register buffer: right after k-step j of the current item has been
+// decoded, register j is refilled with k-step j of the next item, so every wave
+// keeps 23 16-byte loads in flight at all times (a load-then-compute schedule
+// leaves the HBM queues idle while the matrix cores work). The next item's
+// scales, biases and — when its token chunk or K split differs — activation
+// rows are loaded at the start of the current item, ahead of its refills, and
+// written to LDS at its end; loads that are not needed use an empty buffer
+// range (zeros, no memory traffic), so every item issues the same loads in the
+// same order and no wait ever covers a refill that is not yet needed.
+// ---------------------------------------------------------------------------
+constexpr int kStreamWaves = 8;
+constexpr int kStreamThreads = 64 * kStreamWaves;
+constexpr int kSetRows = 16 * kStreamWaves;
+constexpr int kStreamRowLoads = 6;  // 64-unit loads per staged row: K ranges of <= 384 units (96 blocks)
+constexpr int kStreamMaxNB = 96;    // a tile's scales (16 x NB bytes) fit a wave's 1536-byte slice
+
+struct StreamItem {
+    int e, ne, p0, kb0, nblk, split, r0, key;  // key: pass entry and split (same key = same activations)
+};
+
+// Work item f: the items of an expert with np token chunks are numbered
+// ((split * sets) + set) * np + chunk, so an expert's chunks run back to back on
+// the same weight tile (re-reads hit L2) and single-chunk experts step through
+// row sets with the same activations.
+__device__ __forceinline__ StreamItem stream_item(const GemvParams& p, const int4* __restrict__ passes, int f,
+                                                  int sets, int per, int NB, int wave) {
+    const int ipe = sets * p.split;  // items per chunk
+    const int u = f / ipe;           // some chunk of f's expert
+    const int4 pu = passes[u];
+    const int first = u - (pu.w & 0xffff), np = pu.w >> 16;
+    const int l = f - first * ipe;
+    const int chunk = l % np;
+    const int rest = l / np;
+    const int split = rest / sets;
+    const int set = rest - split * sets;
+    const int entry = first + chunk;
+    const int4 pe = passes[entry];
+    StreamItem it;
+    it.e = pe.x;
+    it.ne = pe.y;
+    it.p0 = pe.z;
+    it.split = split;
+    it.kb0 = min(NB, split * per);
+    it.nblk = min(NB, it.kb0 + per) - it.kb0;
+    it.r0 = set * kSetRows + wave * 16;
+    it.key = entry * p.split + split;
+    return it;
+}
+
+// The pass table, sorted pair ids and outputs come in as restrict kernel
+// arguments: the output stores then provably leave the tables alone and the
+// per-item table reads compile to scalar loads, which a wave does not have to
+// order behind its in-flight weight loads.
+template <int MODE>
+__global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p, const int4* __restrict__ passes,
+                                                                   const int32_t* __restrict__ perm,
+                                                                   const int32_t* __restrict__ n_passes,
+                                                                   void* __restrict__ out) {
+    extern __shared__ uint4 lds[];
+    const int NB = p.Kdim >> 5;
+    const int per = (NB + p.split - 1) / p.split;  // <= 92 and NB <= 96: checked by the launcher
+    const int sets = (p.R + kSetRows - 1) / kSetRows;
+    const int total = *n_passes * p.split * sets;
+    const int f0 = (int)((long)total * blockIdx.x / gridDim.x);
+    const int f1 = (int)((long)total * (blockIdx.x + 1) / gridDim.x);
+    if (f0 >= f1) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int m = lane & 15, g = lane >> 4;
+    const int su = 4 * per + 1;  // LDS activation row stride (16-byte units, one-unit pad)
+    const uint32_t row_bytes = (uint32_t)(p.Kdim >> 1);
+    const uint32_t exp_w = (uint32_t)p.R * row_bytes;
+    const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;
+    const uint32_t exp_b = p.bias ? (uint32_t)p.R * 2u : 0u;  // empty range: the bias reads as zero
+    const uint32_t act_bytes = (uint32_t)p.act_rows * (uint32_t)p.Kdim * 2u;
+    uint4* xs = lds;                                                     // [16][su]
+    uint8_t* scl0 = (uint8_t*)(lds + kPassRows * su) + wave * 16 * 96;  // [2 bufs][8 waves][16][NB <= 96]
+    constexpr int kSclBuf = kStreamWaves * 16 * 96;
+
+    // loads of one item's side data: 16 rows of scales, this lane's 4 biases and
+    // (when `act` is set) the item's activation rows 2w, 2w+1 — as 64-unit
+    // lane-contiguous runs at immediate offsets from one scalar row offset
+    u32x4_t sv0, sv1;
+    uint2 bnx;
+    u32x4_t av[2][kStreamRowLoads];
+    auto side_load = [&](const StreamItem& it, bool act) {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales + (size_t)it.e * exp_s, exp_s);
+        sv0 = buf_load16(rs, (uint32_t)it.r0 * NB + lane * 16u, 0);
+        sv1 = buf_load16(rs, (uint32_t)it.r0 * NB + lane * 16u, 1024);
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.bias + (size_t)it.e * p.R, it.split == 0 ? exp_b : 0u);
+        const u32x2_t b2 = __builtin_amdgcn_raw_buffer_load_b64(rb, (uint32_t)(it.r0 + 4 * g) * 2u, 0, 0);
+        bnx = make_uint2(b2[0], b2[1]);
+        const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.act, act ? act_bytes : 0u);
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2) {
+            const int q = min(2 * wave + r2, it.ne - 1);
+            const int row = (MODE == kModeGateUp) ? perm[it.p0 + q] / p.top_k : it.p0 + q;
+            const uint32_t voff = (uint32_t)row * (uint32_t)(p.Kdim * 2) + (uint32_t)(it.kb0 * 4 + lane) * 16u;
+#pragma unroll
+            for (int u = 0; u < kStreamRowLoads; ++u) av[r2][u] = buf_load16(ra, voff, 1024 * u);
+        }
+    };
+    auto scale_store = [&](int b) {  // wave-private slice: no barrier
+        uint8_t* s = scl0 + b * kSclBuf;
+        if (lane < NB) ((u32x4_t*)s)[lane] = sv0;
+        if (lane + 64 < NB) ((u32x4_t*)s)[lane + 64] = sv1;
+    };
+    auto act_store = [&](const StreamItem& it) {
+        __syncthreads();  // every wave has finished reading the previous activations
+        const int cu = 4 * it.nblk;
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2) {
+            const int r = 2 * wave + r2;
+            if (r < it.ne) {
+#pragma unroll
+                for (int u = 0; u < kStreamRowLoads; ++u)
+                    if (lane + 64 * u < cu) ((u32x4_t*)xs)[r * su + lane + 64 * u] = av[r2][u];
+            }
+        }
+        __syncthreads();
+    };
+    auto wrsrc = [&](const StreamItem& it, bool live) {
+        return make_rsrc(p.blocks + (size_t)it.e * exp_w, live ? exp_w : 0u);
+    };
+    auto woffs = [&](const StreamItem& it) {
+        return (uint32_t)(it.r0 + m) * row_bytes + (uint32_t)(it.kb0 + g) * 16u;
+    };
+
+    // prologue: the first item's weights, then its side data
+    StreamItem cur = stream_item(p, passes, f0, sets, per, NB, wave);
+    u32x4_t wq[kGemvNit];
+    {
+        const __amdgpu_buffer_rsrc_t rw = wrsrc(cur, true);
+        const uint32_t voff = woffs(cur);
+#pragma unroll
+        for (int j = 0; j < kGemvNit; ++j) wq[j] = buf_load16(rw, voff, 64 * j);
+    }
+    side_load(cur, true);
+    uint2 bcur = bnx;
+    scale_store(0);
+    act_store(cur);
+    int buf = 0;
+
+    for (int f = f0; f < f1; ++f) {
+        const bool has_next = f + 1 < f1;
+        const StreamItem nxt = stream_item(p, passes, has_next ? f + 1 : f, sets, per, NB, wave);
+        const bool restage = has_next && nxt.key != cur.key;
+        side_load(nxt, restage);
+        const __amdgpu_buffer_rsrc_t rsrc = wrsrc(nxt, has_next);
+        const uint32_t svoff = woffs(nxt);
+        const uint8_t* sl = scl0 + buf * kSclBuf + m * NB + cur.kb0 + g;
+        const uint4* xl = xs + min(m, cur.ne - 1) * su + 4 * g;
+        f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+#pragma unroll
+        for (int j = 0; j < kGemvNit; ++j) {
+            if (4 * j < cur.nblk) {  // wave-uniform
+                const bool edge = 4 * j + 3 >= cur.nblk;
+                const bool bv = 4 * j + g < cur.nblk;
+                uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
+                asm volatile("" : "+v"(sj));
+                const float sf = e8m0_scale_operand(sj);
+                u32x4_t q = wq[j];
+                uint4 x0 = xl[16 * j + 0], x1 = xl[16 * j + 1], x2 = xl[16 * j + 2], x3 = xl[16 * j + 3];
+                if (edge && !bv) {
+                    q = u32x4_t{0u, 0u, 0u, 0u};
+                    x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
+                }
+                acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
+                acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
+                acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
+                acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
+            }
+            // refill after the last read of wq[j]: the load reuses its registers
+            wq[j] = buf_load16(rsrc, svoff, 64 * j);
+            __builtin_amdgcn_sched_barrier(0);  // one refill per k-step
+        }
+        if (cur.r0 < p.R && m < cur.ne) {
+            const f32x4_t acc = (acc0 + acc1) + (acc2 + acc3);
+            const int pp = cur.p0 + m;
+            const int rr = cur.r0 + 4 * g;
+            const float b0 = bf16_lo(bcur.x), b1 = bf16_hi(bcur.x), b2 = bf16_lo(bcur.y), b3 = bf16_hi(bcur.y);
+            if (MODE == kModeGateUp) {
+                const float h0 = swiglu(acc[0] + b0, acc[1] + b1, p.alpha, p.limit);
+                const float h1 = swiglu(acc[2] + b2, acc[3] + b3, p.alpha, p.limit);
+                const int I = p.R >> 1;
+                uint32_t* hout = (uint32_t*)((uint16_t*)out + (size_t)pp * I + (rr >> 1));
+                *hout = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
+            } else {
+                float4 y;
+                y.x = acc[0] + b0;
+                y.y = acc[1] + b1;
+                y.z = acc[2] + b2;
+                y.w = acc[3] + b3;
+                float* ybase = (float*)out + (size_t)cur.split * p.n_pairs * p.R;
+                *(float4*)(ybase + (size_t)pp * p.R + rr) = y;
+            }
+        }
+        if (!has_next) break;
+        buf ^= 1;
+        scale_store(buf);
+        bcur = bnx;
+        if (restage) act_store(nxt);
+        cur = nxt;
+    }
+}
+
 // out[t, d] = bf16( sum_j w[t,j] * y[pos[t*k+j], d] ), fp32 fma in k order
 // (kernels/moe_combine.hip:16-20, batched). With a K-split down projection, y is
 // the sum of the split partials, added in split order first. Each lane handles 4
@@ -410,7 +621,8 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
     if (NB > kMaxScaleBlocks) return set_error(PHYSLLM_MOE_EINVAL, "gemv: reduction dimension > 8192");
     static bool attr_set = false;
     if (!attr_set) {
-        const void* ks[] = {(const void*)k_mx_gemv<kModeGateUp, 2>, (const void*)k_mx_gemv<kModeGateUp, 12>,
+        const void* ks[] = {(const void*)k_mx_gemv_stream<kModeGateUp>, (const void*)k_mx_gemv_stream<kModeDown>,
+                            (const void*)k_mx_gemv<kModeGateUp, 2>, (const void*)k_mx_gemv<kModeGateUp, 12>,
                             (const void*)k_mx_gemv<kModeDown, 2>, (const void*)k_mx_gemv<kModeDown, 12>,
                             (const void*)k_mx_gemv_generic<kModeGateUp>, (const void*)k_mx_gemv_generic<kModeDown>};
         for (const void* k : ks) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -420,7 +632,26 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
     const int ntok = max_tokens < kPassTok ? max_tokens : kPassTok;
     const int rows_per_set = (kGemvThreads / 64) * 16;
     const int sets = (p.R + rows_per_set - 1) / rows_per_set;
-    if (per <= 4 * kGemvNit) {
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    const long stream_items = (long)((p.R + kSetRows - 1) / kSetRows) * max_slots * p.split;
+    const bool fast = per <= 4 * kGemvNit && NB <= kStreamMaxNB;
+    if (fast && p.passes && max_tokens > 1 && stream_items >= 2L * n_cu) {
+        // many touched experts: persistent streaming kernel, one 8-wave group per CU
+        const size_t lds = (size_t)kPassRows * (4 * per + 1) * 16 + (size_t)2 * kStreamWaves * 16 * 96;
+        p.rt = 1;
+        if (mode == kModeGateUp)
+            hipLaunchKernelGGL(k_mx_gemv_stream<kModeGateUp>, dim3(n_cu), dim3(kStreamThreads), lds, stream, p,
+                               p.passes, p.perm, p.n_passes, p.out);
+        else
+            hipLaunchKernelGGL(k_mx_gemv_stream<kModeDown>, dim3(n_cu), dim3(kStreamThreads), lds, stream, p,
+                               p.passes, p.perm, p.n_passes, p.out);
+    } else if (fast) {
         // activation units one thread stages per pass: ntok rows x 4*per 16-byte units
         const int units = ntok * 4 * per;
         const int ns = (units + kGemvThreads - 1) / kGemvThreads;

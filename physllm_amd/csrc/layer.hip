@@ -46,6 +46,8 @@ struct Workspace {
     int4* slots;
     int32_t* n_slots;
     int32_t* tprefix;  // [E+1] token-tile prefix over slots
+    int4* passes;      // [N/16 + E] pass table (decode)
+    int32_t* n_passes;
     int32_t* perm;
     int32_t* pos;
     uint16_t* h;
@@ -92,6 +94,9 @@ static Workspace carve(const physllm_moe_config& c, int B, char* base) {
     w.slots = (int4*)take(E * 16);
     w.n_slots = (int32_t*)take(4);
     w.tprefix = (int32_t*)take((E + 1) * 4);
+    const bool decode = !use_gemm(c, B);
+    w.passes = (int4*)take(decode ? (N / kPassRows + std::min(N, E)) * 16 : 0);
+    w.n_passes = (int32_t*)take(4);
     w.perm = (int32_t*)take(N * 4);
     w.pos = (int32_t*)take(N * 4);
     w.h = (uint16_t*)take(N * (size_t)c.intermediate * 2);
@@ -153,8 +158,10 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
     if (stages & kStageRoute) {
         if ((rc = router_launch(x, w->router_w, w->router_b, batch, c.hidden, c.num_experts, c.top_k, idx, wts, s)))
             return rc;
+        // prefill: the GEMM's token-tile prefix; decode: the GEMV's pass table
+        const bool gemm = use_gemm(c, batch);
         if ((rc = bucket_launch(idx, N, c.num_experts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.slots, ws.n_slots,
-                                ws.tprefix, kGemmTileN, s)))
+                                gemm ? ws.tprefix : nullptr, kGemmTileN, gemm ? nullptr : ws.passes, ws.n_passes, s)))
             return rc;
     }
     const int max_slots = N < c.num_experts ? N : c.num_experts;
@@ -162,6 +169,8 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
     p.perm = ws.perm;
     p.slots = ws.slots;
     p.n_slots = ws.n_slots;
+    p.passes = ws.passes;
+    p.n_passes = ws.n_passes;
     p.top_k = c.top_k;
     p.split = 1;
     p.n_pairs = N;

@@ -1,19 +1,21 @@
 // Router (GEMV + top-k + softmax) and token bucketing for gfx950.
 //
 // Router semantics (kernels/moe_router.hip:24-78 of the reference, with a bias):
-//   logits[b,e] = sum_d x[b,d] * W[e,d]  — every bf16*bf16 product is exact in
-//   fp32 and is accumulated in fp64, then + bias[e]; top-k by repeated selection of
-//   the largest unused logit (strict '>', so ties go to the lowest index; NaN ranks
-//   lowest); softmax over the k selected, in fp64, rounded to fp32.
+//   logits[b,e] = sum_d fl32(x[b,d] * W[e,d]) accumulated in fp64, + bias[e] —
+//   each product formed in fp32 as the reference does (exact for bf16 operands in
+//   the fp32 normal range); top-k by repeated selection of the largest unused
+//   logit (strict '>', so ties go to the lowest index; NaN ranks lowest); softmax
+//   over the k selected, in fp64, rounded to fp32.
 // fp64 accumulation makes the logits independent of the summation order to far
-// below any realistic top-k gap, so this kernel's indices equal the CPU oracle's
-// serial sums bit for bit.
+// below any realistic top-k gap, so the indices equal the CPU oracle's serial
+// sums bit for bit.
 //
 // Layout: one workgroup of 8 waves handles TB tokens. Wave w computes experts
 // w*EPI.., with every lane's 16-byte chunks of all EPI router rows and TB token
 // rows loaded up front (a wave reads contiguous 1 KiB slices of each row), then a
-// butterfly reduction per dot. Logits go to LDS; then one wave per token runs
-// the selection with a wave-wide arg-max per round.
+// DPP/permlane reduction per dot. Logits go to LDS; then one wave per token ranks
+// them (rank_select: one pass of broadcast LDS reads instead of k dependent
+// arg-max rounds) and writes the selection and its softmax.
 #include "common.h"
 #include "capi_internal.h"
 #include "experts.h"
@@ -34,21 +36,137 @@ __device__ __forceinline__ bool rank_beats(double av, int ae, double bv, int be)
     return ae < be;
 }
 
-__device__ __forceinline__ void bf16x8_to_f64(uint4 v, double (&d)[8]) {
-    d[0] = (double)bf16_lo(v.x);
-    d[1] = (double)bf16_hi(v.x);
-    d[2] = (double)bf16_lo(v.y);
-    d[3] = (double)bf16_hi(v.y);
-    d[4] = (double)bf16_lo(v.z);
-    d[5] = (double)bf16_hi(v.z);
-    d[6] = (double)bf16_lo(v.w);
-    d[7] = (double)bf16_hi(v.w);
+// Top-k of one token's logits L[0..E) by one wave: K rounds of a wave-wide
+// arg-max over the unused experts (moe_router.hip:35-58 selects by repeated
+// scans the same way), then the softmax over the k selected, in selection order
+// (moe_router.hip:61-78), in fp64 and rounded to fp32.
+__device__ __forceinline__ void select_topk(const double* L, int E, int K, int lane, int32_t* idx_row,
+                                            float* w_row) {
+    uint32_t used = 0;  // bit i: expert lane + 64 i taken
+    double my_sel = 0.0;
+    int my_idx = 0;
+    for (int j = 0; j < K; ++j) {
+        double bv = 0.0;
+        int be = -1;
+        for (int i = 0; lane + 64 * i < E; ++i) {
+            const int e = lane + 64 * i;
+            if (used & (1u << i)) continue;
+            const double v = L[e];
+            if (rank_beats(v, e, bv, be)) { bv = v; be = e; }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const double ov = __shfl_xor(bv, o, 64);
+            const int oe = __shfl_xor(be, o, 64);
+            if (rank_beats(ov, oe, bv, be)) { bv = ov; be = oe; }
+        }
+        if (be >= 0 && (be & 63) == lane) used |= 1u << (be >> 6);
+        if (lane == j) { my_sel = bv; my_idx = be; }
+    }
+    double m = __shfl(my_sel, 0, 64);
+    for (int j = 1; j < K; ++j) m = fmax(m, __shfl(my_sel, j, 64));
+    const double ex = (lane < K) ? exp(my_sel - m) : 0.0;
+    double sum = 0.0;
+    for (int j = 0; j < K; ++j) sum += __shfl(ex, j, 64);
+    if (lane < K) {
+        idx_row[lane] = my_idx;
+        w_row[lane] = (float)(ex / sum);
+    }
+}
+
+// Orderable key of an fp64 logit: a larger value has a larger key, NaN has the
+// lowest key (0), -0 and +0 share one. With ties broken by the lower index this
+// is rank_beats' order.
+__device__ __forceinline__ uint64_t order_key(double v) {
+    if (__builtin_isnan(v)) return 0ull;
+    const uint64_t b = (uint64_t)__double_as_longlong(v == 0.0 ? 0.0 : v);
+    return (b >> 63) ? ~b : (b | (1ull << 63));
+}
+
+// Per-wave LDS scratch of rank_select: keys [256], ids [256], values [2][32].
+constexpr int kRankMax = 256;
+constexpr size_t kRankScratchBytes = kRankMax * 8 + kRankMax * 4 + 64 * 8;
+
+// rank[i] = number of the n values (slot lane + 64 i holds vals[i], ids[i]) that
+// beat value i in rank_beats' order: one pass of broadcast LDS reads per wave.
+__device__ __forceinline__ void compute_ranks(const double (&vals)[4], const int (&ids)[4], int n, int lane,
+                                              void* scratch, int (&rank)[4]) {
+    uint64_t* ks = (uint64_t*)scratch;
+    int* is = (int*)(ks + kRankMax);
+    uint64_t key[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        key[i] = order_key(vals[i]);
+        rank[i] = 0;
+        if (lane + 64 * i < n) {
+            ks[lane + 64 * i] = key[i];
+            is[lane + 64 * i] = ids[i];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int s2 = 0; s2 < n; ++s2) {
+        const uint64_t k2 = ks[s2];
+        const int e2 = is[s2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rank[i] += (k2 > key[i] || (k2 == key[i] && e2 < ids[i])) ? 1 : 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Top-k and softmax of n <= 256 values by one wave, select_topk's results
+// without its K dependent arg-max rounds: value i of slot lane + 64 i (id ids[i],
+// absent when the slot is >= n) gets rank = number of values that beat it, from
+// one pass over the keys in LDS; ranks 0..K-1 are the selection in order.
+__device__ __forceinline__ void rank_select(const double (&vals)[4], const int (&ids)[4], int n, int K, int lane,
+                                            void* scratch, int32_t* idx_row, float* w_row) {
+    double* sv = (double*)((char*)scratch + kRankMax * 12);  // [0, 32): selected values; [32, 64): their exps
+    int rank[4];
+    compute_ranks(vals, ids, n, lane, scratch, rank);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (lane + 64 * i < n && rank[i] < K) {
+            sv[rank[i]] = vals[i];
+            idx_row[rank[i]] = ids[i];
+        }
+    __builtin_amdgcn_wave_barrier();
+    const double m = sv[0];  // fmax over the selection = the first pick (NaN only if all are NaN)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (lane + 64 * i < n && rank[i] < K) sv[32 + rank[i]] = exp(vals[i] - m);
+    __builtin_amdgcn_wave_barrier();
+    double sum = 0.0;
+    for (int j = 0; j < K; ++j) sum += sv[32 + j];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (lane + 64 * i < n && rank[i] < K) w_row[rank[i]] = (float)(sv[32 + rank[i]] / sum);
+    __builtin_amdgcn_wave_barrier();  // scratch reusable
+}
+
+__device__ __forceinline__ void bf16x8_to_f32(uint4 v, float (&f)[8]) {
+    f[0] = bf16_lo(v.x);
+    f[1] = bf16_hi(v.x);
+    f[2] = bf16_lo(v.y);
+    f[3] = bf16_hi(v.y);
+    f[4] = bf16_lo(v.z);
+    f[5] = bf16_hi(v.z);
+    f[6] = bf16_lo(v.w);
+    f[7] = bf16_hi(v.w);
+}
+
+// acc + fl32(a * b) in fp64: the product is formed in fp32 as the reference's
+// router does (exact for bf16 operands inside the fp32 normal range, inf past
+// it, a rounded subnormal below it) and accumulated in fp64. Contraction is off:
+// an fp64 fma would skip the fp32 rounding of the product.
+__device__ __forceinline__ double acc_prod(double acc, float a, float b) {
+#pragma clang fp contract(off)
+    const float p = a * b;
+    return acc + (double)p;
 }
 
 // Logits of TB tokens x EPI experts for one wave: each lane owns 8-element chunks
 // c = lane + 64 u; all U chunks of every operand are loaded before any is used, so
 // a wave has (EPI + TB) * U 16-byte loads in flight instead of one round trip per
-// chunk. bf16 products are exact in fp64 and summed in fp64.
+// chunk. Products in fp32, sums in fp64 (acc_prod).
 template <int TB, int EPI, int U>
 __device__ __forceinline__ void router_dots(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int t0,
                                             int ntb, int e0, int E, int H, int lane, double (&acc)[EPI][TB]) {
@@ -73,17 +191,17 @@ __device__ __forceinline__ void router_dots(const uint16_t* __restrict__ x, cons
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            double xd[TB][8];
+            float xf[TB][8];
 #pragma unroll
-            for (int tb = 0; tb < TB; ++tb) bf16x8_to_f64(xv[tb][u], xd[tb]);
+            for (int tb = 0; tb < TB; ++tb) bf16x8_to_f32(xv[tb][u], xf[tb]);
 #pragma unroll
             for (int ei = 0; ei < EPI; ++ei) {
-                double wd[8];
-                bf16x8_to_f64(wv[ei][u], wd);
+                float wf[8];
+                bf16x8_to_f32(wv[ei][u], wf);
 #pragma unroll
                 for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) acc[ei][tb] = __builtin_fma(xd[tb][i], wd[i], acc[ei][tb]);
+                    for (int i = 0; i < 8; ++i) acc[ei][tb] = acc_prod(acc[ei][tb], xf[tb][i], wf[i]);
             }
         }
     }
@@ -114,11 +232,11 @@ __global__ __launch_bounds__(kRouterThreads) void k_router(const uint16_t* __res
 #pragma unroll
                 for (int ei = 0; ei < EPI; ++ei) {
                     if (e0 + ei >= E) continue;
-                    const double wv = (double)bf16_to_f32(w[(size_t)(e0 + ei) * H + d]);
+                    const float wv = bf16_to_f32(w[(size_t)(e0 + ei) * H + d]);
 #pragma unroll
                     for (int tb = 0; tb < TB; ++tb)
                         if (tb < ntb)
-                            acc[ei][tb] = __builtin_fma((double)bf16_to_f32(x[(size_t)(t0 + tb) * H + d]), wv, acc[ei][tb]);
+                            acc[ei][tb] = acc_prod(acc[ei][tb], bf16_to_f32(x[(size_t)(t0 + tb) * H + d]), wv);
                 }
             }
         }
@@ -135,39 +253,20 @@ __global__ __launch_bounds__(kRouterThreads) void k_router(const uint16_t* __res
     }
     __syncthreads();
 
+    void* rscr = (void*)(lg + TB * E + wave * (kRankScratchBytes / 8));
     for (int tb = wave; tb < ntb; tb += NW) {
         const int t = t0 + tb;
-        const double* L = lg + tb * E;
-        uint32_t used = 0;  // bit i: expert lane + 64 i taken
-        double my_sel = 0.0;
-        int my_idx = 0;
-        for (int j = 0; j < K; ++j) {
-            double bv = 0.0;
-            int be = -1;
-            for (int i = 0; lane + 64 * i < E; ++i) {
-                const int e = lane + 64 * i;
-                if (used & (1u << i)) continue;
-                const double v = L[e];
-                if (rank_beats(v, e, bv, be)) { bv = v; be = e; }
-            }
+        if (E <= kRankMax) {
+            double vals[4];
+            int ids[4];
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const double ov = __shfl_xor(bv, o, 64);
-                const int oe = __shfl_xor(be, o, 64);
-                if (rank_beats(ov, oe, bv, be)) { bv = ov; be = oe; }
+            for (int i = 0; i < 4; ++i) {
+                ids[i] = lane + 64 * i;
+                vals[i] = ids[i] < E ? lg[tb * E + ids[i]] : 0.0;
             }
-            if (be >= 0 && (be & 63) == lane) used |= 1u << (be >> 6);
-            if (lane == j) { my_sel = bv; my_idx = be; }
-        }
-        // softmax over the k selected, in selection order (moe_router.hip:61-78)
-        double m = __shfl(my_sel, 0, 64);
-        for (int j = 1; j < K; ++j) m = fmax(m, __shfl(my_sel, j, 64));
-        const double ex = (lane < K) ? exp(my_sel - m) : 0.0;
-        double sum = 0.0;
-        for (int j = 0; j < K; ++j) sum += __shfl(ex, j, 64);
-        if (lane < K) {
-            idx[(size_t)t * K + lane] = my_idx;
-            wts[(size_t)t * K + lane] = (float)(ex / sum);
+            rank_select(vals, ids, E, K, lane, rscr, idx + (size_t)t * K, wts + (size_t)t * K);
+        } else {
+            select_topk(lg + tb * E, E, K, lane, idx + (size_t)t * K, wts + (size_t)t * K);
         }
     }
 }
@@ -184,11 +283,12 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
         // prefill: 4 tokens per group share every loaded router row
         constexpr int TB = 4;
         hipLaunchKernelGGL((k_router<TB, 1, 4>), dim3((B + TB - 1) / TB), dim3(kRouterThreads),
-                           (size_t)TB * E * sizeof(double), stream, (const uint16_t*)x, (const uint16_t*)w,
+                           (size_t)TB * E * sizeof(double) + (kRouterThreads / 64) * kRankScratchBytes, stream, (const uint16_t*)x, (const uint16_t*)w,
                            (const uint16_t*)bias, B, H, E, K, (int32_t*)idx, (float*)wts, vec);
     } else {
         // decode: one token per group, 4 experts' rows in flight per wave
-        hipLaunchKernelGGL((k_router<1, 4, 6>), dim3(B), dim3(kRouterThreads), (size_t)E * sizeof(double), stream,
+        hipLaunchKernelGGL((k_router<1, 4, 6>), dim3(B), dim3(kRouterThreads),
+                           (size_t)E * sizeof(double) + (kRouterThreads / 64) * kRankScratchBytes, stream,
                            (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, B, H, E, K,
                            (int32_t*)idx, (float*)wts, vec);
     }
@@ -211,21 +311,24 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
 // ---------------------------------------------------------------------------
 constexpr int kBucketThreads = 1024;
 
+// Exclusive prefix over the first n <= 1024 threads' values (later threads
+// contribute 0): shuffle scans inside each wave, then the wave totals; two
+// barriers. sbuf holds 16 ints.
 __device__ __forceinline__ int block_excl_scan(int v, int* sbuf, int n) {
-    // Hillis-Steele over n <= 1024 entries held one per thread; returns exclusive prefix.
-    const int tid = threadIdx.x;
-    if (tid < n) sbuf[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < n; off <<= 1) {
-        int add = 0;
-        if (tid < n && tid >= off) add = sbuf[tid - off];
-        __syncthreads();
-        if (tid < n) sbuf[tid] += add;
-        __syncthreads();
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int mine = (tid < n) ? v : 0;
+    int x = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
     }
-    const int incl = (tid < n) ? sbuf[tid] : 0;
+    if (lane == 63) sbuf[wave] = x;
     __syncthreads();
-    return incl - ((tid < n) ? v : 0);
+    int base = 0;
+    for (int w2 = 0; w2 < wave; ++w2) base += sbuf[w2];
+    __syncthreads();  // sbuf may be reused by the next scan
+    return base + x - mine;
 }
 
 __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __restrict__ idx, int N, int E,
@@ -233,13 +336,14 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
                                                            int32_t* __restrict__ offsets,
                                                            int32_t* __restrict__ perm, int32_t* __restrict__ pos,
                                                            int4* __restrict__ slots, int32_t* __restrict__ n_slots,
-                                                           int32_t* __restrict__ tprefix, int tile_n) {
+                                                           int32_t* __restrict__ tprefix, int tile_n,
+                                                           int4* __restrict__ passes, int32_t* __restrict__ n_passes) {
     extern __shared__ int smem[];
     int* cnt = smem;                   // [E]
     int* off = cnt + E;                // [E]
     int* run = off + E;                // [E]
-    int* scan = run + E;               // [1024]
-    int* wcnt = scan + kBucketThreads; // [16][E]
+    int* scan = run + E;               // [16] wave totals of the block scans
+    int* wcnt = scan + 16;             // [16][E]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nwaves = kBucketThreads / 64;
 
@@ -275,6 +379,18 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
                 const int tex = block_excl_scan(nt, scan, E);
                 if (tid < E && c > 0) tprefix[na] = tex;
                 if (tid == E - 1) tprefix[ntouched] = tex + nt;
+            }
+            if (passes) {
+                // each touched expert's sorted positions in chunks of kPassRows:
+                // {expert, tokens, first position, chunk index | chunk count << 16}
+                // (chunk counts stay below 2^16: the GEMV path has < 64 E pairs)
+                const int np = (c + kPassRows - 1) / kPassRows;
+                const int pex = block_excl_scan(np, scan, E);
+                if (tid < E)
+                    for (int t = 0; t < np; ++t)
+                        passes[pex + t] =
+                            make_int4(tid, min(kPassRows, c - t * kPassRows), ex + t * kPassRows, t | (np << 16));
+                if (tid == E - 1 && n_passes) *n_passes = pex + np;
             }
         }
     }
@@ -313,10 +429,10 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
     }
 }
 
-size_t bucket_smem_bytes(int E) { return sizeof(int) * ((size_t)3 * E + kBucketThreads + 16 * (size_t)E); }
+size_t bucket_smem_bytes(int E) { return sizeof(int) * ((size_t)3 * E + 16 + 16 * (size_t)E); }
 
 int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, void* perm, void* pos, void* slots,
-                  void* n_slots, void* tprefix, int tile_n, hipStream_t stream) {
+                  void* n_slots, void* tprefix, int tile_n, void* passes, void* n_passes, hipStream_t stream) {
     static bool attr_set = false;
     const size_t smem = bucket_smem_bytes(E);
     if (!attr_set) {
@@ -326,7 +442,7 @@ int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, vo
     }
     hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBucketThreads), smem, stream, (const int32_t*)idx, N, E,
                        (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm, (int32_t*)pos, (int4*)slots,
-                       (int32_t*)n_slots, (int32_t*)tprefix, tile_n);
+                       (int32_t*)n_slots, (int32_t*)tprefix, tile_n, (int4*)passes, (int32_t*)n_passes);
     return check_launch("bucket");
 }
 
@@ -347,7 +463,7 @@ extern "C" int physllm_moe_bucket(const void* idx, int batch, int top_k, int num
     if ((int64_t)batch * top_k > 0x7fffffffLL) return set_error(PHYSLLM_MOE_EINVAL, "bucket: batch*top_k too large");
     if (!idx || !counts || !offsets || !perm || !pos) return set_error(PHYSLLM_MOE_EINVAL, "bucket: null pointer");
     return bucket_launch(idx, batch * top_k, num_experts, counts, offsets, perm, pos, nullptr, nullptr, nullptr, 1,
-                         (hipStream_t)stream);
+                         nullptr, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int physllm_moe_route_topk(const void* x, const void* router_w, const void* router_b, int batch,

@@ -141,6 +141,53 @@ def test_router_ties_and_nan(oracle):
     assert np.array_equal(np.isnan(gw), np.isnan(ew))
 
 
+def _router_case(oracle, x, w, b, K):
+    B = x.shape[0]
+    idx = torch.empty((B, K), dtype=torch.int32, device="cuda")
+    wt = torch.empty((B, K), dtype=torch.float32, device="cuda")
+    ops.route_topk(dev(x), dev(w), None if b is None else dev(b), idx, wt, K, stream())
+    torch.cuda.synchronize()
+    eidx, ew = oracle.router(x, w, b, K)
+    assert np.array_equal(host(idx), eidx)
+    assert np.allclose(host(wt), ew, rtol=1e-6, atol=1e-7, equal_nan=True)
+    return host(idx)
+
+
+def test_router_near_ties_decided_in_fp64(oracle):
+    """Experts whose logits differ by one bf16 ulp of one weight (far below the
+    fp32 matrix-core error bound): the order comes from the fp64 recomputation.
+    Experts 3 and 7 lead every token; 10, 11 and 12 compete for the 4th pick."""
+    rng = np.random.default_rng(5)
+    B, H, E, K = 48, 2880, 32, 4
+    xf = rng.standard_normal((B, H), dtype=np.float32)
+    xf[:, 100] = np.abs(xf[:, 100]) + 0.5          # d = 100 has x > 0 for every token
+    x = syn.bf16_from_f32(xf)
+    w = syn.bf16_from_f32(rng.standard_normal((E, H), dtype=np.float32) * np.float32(0.02))
+    w[7] = w[3]
+    w[7, 100] += 1                                   # +1 ulp (same sign as the value's magnitude step)
+    w[11] = w[10]
+    w[12] = w[10]
+    w[12, 100] -= 1
+    bf = np.zeros(E, np.float32)
+    bf[[3, 7]] = 8.0
+    bf[[10, 11, 12]] = 4.0
+    b = syn.bf16_from_f32(bf)
+    got = _router_case(oracle, x, w, b, K)
+    assert set(got[:, :2].ravel()) <= {3, 7}
+
+
+@pytest.mark.parametrize("scale", [2.0 ** 66, 2.0 ** -70])
+def test_router_fp32_overflow_and_subnormal_products(oracle, scale):
+    """Products beyond the fp32 range (x, w ~ 2^66) or below its normal range
+    (~2^-140): the matrix-core pass yields non-finite or flushed sums, every
+    affected expert becomes a candidate and the fp64 pass ranks them."""
+    rng = np.random.default_rng(6)
+    B, H, E, K = 20, 2880, 32, 4
+    x = syn.bf16_from_f32((rng.standard_normal((B, H)) * scale).astype(np.float32))
+    w = syn.bf16_from_f32((rng.standard_normal((E, H)) * scale).astype(np.float32))
+    _router_case(oracle, x, w, None, K)
+
+
 @pytest.mark.parametrize("B,K,E,skew", [(1, 4, 32, False), (64, 4, 32, True), (4096, 4, 32, False),
                                         (256, 4, 128, False), (3000, 1, 3, True)])
 def test_bucket_matches_oracle(oracle, B, K, E, skew):
@@ -194,8 +241,11 @@ def test_layer_tiny_against_oracle_and_float64(oracle):
     assert refmath.rel_l2(refmath.bf16_bits_to_f64(got), ref) < 4e-3
 
 
-@pytest.mark.parametrize("E,H,I,K,B", [(8, 256, 128, 3, 20), (16, 512, 1024, 4, 40), (3, 96, 160, 1, 37)])
+@pytest.mark.parametrize("E,H,I,K,B", [(8, 256, 128, 3, 20), (16, 512, 1024, 4, 40), (3, 96, 160, 1, 37),
+                                       (8, 256, 4096, 2, 1), (8, 128, 3200, 2, 3)])
 def test_layer_odd_shapes(oracle, E, H, I, K, B):
+    """Includes down projections whose reduction (I = 4096, 3200) is split over
+    several K ranges at small batch: 128 and 100 scale blocks per row."""
     layer = syn.make_layer(E, H, I, K, seed=E + B)
     x = syn.make_x(B, H, seed=B)
     _check_layer(oracle, layer, x, f"E={E} H={H} I={I} K={K} B={B}")
@@ -210,6 +260,24 @@ def test_layer_grouped_gemm_path(oracle, E, H, I, K, B):
     layer = syn.make_layer(E, H, I, K, seed=E * 100 + B)
     x = syn.make_x(B, H, seed=B)
     _check_layer(oracle, layer, x, f"gemm E={E} H={H} I={I} K={K} B={B}")
+
+
+@pytest.mark.parametrize("E,H,I,K,B,hot,bias", [(128, 288, 352, 4, 100, None, True),
+                                                (128, 288, 352, 4, 100, 3, True),
+                                                (128, 288, 352, 4, 100, None, False),
+                                                (64, 2880, 2880, 4, 16, None, True)])
+def test_layer_streaming_gemv(oracle, E, H, I, K, B, hot, bias):
+    """Decode batches touching many experts (>= 2 work items per CU) take the
+    persistent streaming GEMV: K ranges ending inside a 4-block step (9 and 11
+    blocks), weight rows not a multiple of 128 (704, 288), an expert holding every
+    token (100 tokens: 7 pass-table entries, restaged activations), no biases."""
+    layer = syn.make_layer(E, H, I, K, seed=E + H + B, with_bias=bias)
+    if hot is not None:
+        rb = syn.bf16_to_f32(layer.router_b).copy()
+        rb[hot] = 50.0
+        layer.router_b = syn.bf16_from_f32(rb)
+    x = syn.make_x(B, H, seed=B + 1)
+    _check_layer(oracle, layer, x, f"stream E={E} H={H} I={I} K={K} B={B} hot={hot} bias={bias}")
 
 
 def test_layer_without_biases(oracle):

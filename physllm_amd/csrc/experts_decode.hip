@@ -445,7 +445,6 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
     const int lane = threadIdx.x & 63;
     const int m = lane & 15, g = lane >> 4;
     const int su = 4 * per + 1;  // LDS activation row stride (16-byte units, one-unit pad)
-    constexpr uint32_t kPastRange = 0x80000000u;  // voffset past every expert's range: the load returns zeros
     const uint32_t row_bytes = (uint32_t)(p.Kdim >> 1);
     const uint32_t exp_w = (uint32_t)p.R * row_bytes;
     const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;
@@ -511,7 +510,7 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
         const __amdgpu_buffer_rsrc_t rw = wrsrc(cur, true);
         const uint32_t voff = woffs(cur);
 #pragma unroll
-        for (int j = 0; j < kGemvNit; ++j) wq[j] = buf_load16(rw, 4 * j < cur.nblk ? voff : kPastRange, 64 * j);
+        for (int j = 0; j < kGemvNit; ++j) wq[j] = buf_load16(rw, voff, 64 * j);
     }
     side_load(cur, true);
     uint2 bcur = bnx;
@@ -549,8 +548,7 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
                 acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
             }
             // refill after the last read of wq[j]: the load reuses its registers
-            // (k-steps past the next item's K range read zeros, no memory traffic)
-            wq[j] = buf_load16(rsrc, 4 * j < nxt.nblk ? svoff : kPastRange, 64 * j);
+            wq[j] = buf_load16(rsrc, svoff, 64 * j);
             __builtin_amdgcn_sched_barrier(0);  // one refill per k-step
         }
         if (cur.r0 < p.R && m < cur.ne) {
@@ -643,8 +641,9 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
     }
     const long stream_items = (long)((p.R + kSetRows - 1) / kSetRows) * max_slots * p.split;
     const bool fast = per <= 4 * kGemvNit && NB <= kStreamMaxNB;
-    // (the streaming kernel's out-of-range offset 2^31 must exceed an expert's bytes)
-    const bool stream_ok = (int64_t)p.R * (p.Kdim / 2) < 0x80000000LL;
+    // The streaming kernel takes whole K rows (no split: it loads the 23 k-steps of
+    // a tile as one row segment) of experts below 2 GiB (32-bit buffer offsets).
+    const bool stream_ok = p.split == 1 && (int64_t)p.R * (p.Kdim / 2) < 0x80000000LL;
     if (fast && stream_ok && p.passes && max_tokens > 1 && stream_items >= 2L * n_cu) {
         // many touched experts: persistent streaming kernel, one 8-wave group per CU
         const size_t lds = (size_t)kPassRows * (4 * per + 1) * 16 + (size_t)2 * kStreamWaves * 16 * 96;

@@ -19,6 +19,9 @@
 // y fp32. Tiles are scheduled from a device-side per-expert prefix of token
 // tiles, and consecutive token tiles of one weight row tile are mapped to the
 // same XCD so they share its L2.
+// Two forms: k_mx_gemm2 (256 x 128 tiles, 8 waves, loads two k-steps ahead,
+// the tile's scales staged in LDS) for K up to 96 MX blocks, and k_mx_gemm
+// (128 x 128, 4 waves) for longer K.
 #include "common.h"
 #include "capi_internal.h"
 #include "experts.h"
@@ -204,17 +207,234 @@ __global__ __launch_bounds__(kGemmThreads, 2) void k_mx_gemm(GemvParams p, const
     }
 }
 
+// ---------------------------------------------------------------------------
+// Wide-tile form: one workgroup of 8 waves (4 x 2, 64 x 64 each) computes 256
+// weight rows x 128 tokens, halving the activation re-reads per flop of the
+// 128 x 128 form. Loads run kGemmPD k-steps ahead of the MFMAs:
+//   A (weights): each lane's 4 stripes of a k-step in a register ring;
+//   B (activations): staged through registers into a double-buffered LDS tile
+//     (the registers of step ks + 1 were filled during step ks - 1);
+//   scales: the tile's 256 rows x NB bytes, staged into LDS once.
+// Waves whose 64 rows all lie past R skip their MFMAs.
+// ---------------------------------------------------------------------------
+constexpr int kG2Threads = 512;
+constexpr int kG2TM = 256;
+constexpr int kG2BUnits = kTN * (kKS * 2 / 16) / kG2Threads;  // 4 B units per thread per k-step
+constexpr int kG2MaxNB = 96;                                   // scale row bytes staged per tile row
+constexpr int kG2BRow = kBRowU;                                // LDS row stride of the B tile (16-byte units)
+
+template <int MODE>
+__global__ __launch_bounds__(kG2Threads, 1) void k_mx_gemm2(GemvParams p, const int32_t* __restrict__ tprefix) {
+    extern __shared__ uint4 lds[];
+    const int G = gridDim.x;  // a multiple of 8
+    const int bid = blockIdx.x;
+    const int t = (bid & 7) * (G >> 3) + (bid >> 3);
+    const int n_slots = *p.n_slots;
+    const int row_tiles = (p.R + kG2TM - 1) / kG2TM;
+    if (t >= row_tiles * tprefix[n_slots]) return;
+    int lo = 0, hi = n_slots;  // largest s with row_tiles * tprefix[s] <= t
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (row_tiles * tprefix[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int slot = lo;
+    const int4 si = p.slots[slot];
+    const int e = si.x, ne = si.y, p0 = si.z;
+    const int ntt = (ne + kTN - 1) / kTN;
+    const int local = t - row_tiles * tprefix[slot];
+    const int rtile = local / ntt;
+    const int ttile = local - rtile * ntt;
+    const int row0 = rtile * kG2TM;
+    const int tok0 = ttile * kTN;
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int m = lane & 15, g = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;  // rows 64*wm.., tokens 64*wn..
+    const bool wave_rows = row0 + wm * 64 < p.R;  // wave-uniform
+    const int NB = p.Kdim >> 5;
+    const int nks = (NB + 3) >> 2;
+    const uint32_t row_bytes = (uint32_t)(p.Kdim >> 1);
+    const uint32_t exp_w = (uint32_t)p.R * row_bytes;
+    const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;
+    const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(p.blocks + (size_t)e * exp_w, exp_w);
+    const __amdgpu_buffer_rsrc_t rsc = gemm_rsrc(p.scales + (size_t)e * exp_s, exp_s);
+    const __amdgpu_buffer_rsrc_t ract = gemm_rsrc(p.act, (uint32_t)p.act_rows * (uint32_t)p.Kdim * 2u);
+
+    uint4* bsm = lds;                                        // [2][kTN][kG2BRow]
+    // scales of the tile's rows, all of K, as [4 row blocks wm][16 rows m][NB][4 tiles mt]:
+    // the 4 scales a lane needs for one block are one dword
+    uint32_t* ssm = (uint32_t*)(lds + 2 * kTN * kG2BRow);
+
+    // ---- stage the scales: 16-byte global loads of the 256 x NB bytes, scattered
+    // byte by byte into the transposed layout ----
+    {
+        const int nunits = (kG2TM * NB + 15) / 16;
+        const uint32_t sbase = (uint32_t)row0 * NB;
+        uint8_t* sb = (uint8_t*)ssm;
+        for (int u = threadIdx.x; u < nunits; u += kG2Threads) {
+            const u32x4_t v = gemm_load16(rsc, sbase + 16u * u);  // rows past R read zeros
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int idx = 16 * u + k;  // byte of the tile: row r = idx / NB, block idx % NB
+                if (idx < kG2TM * NB) {
+                    const int r = idx / NB, blk = idx - r * NB;
+                    const int wmr = r >> 6, mt = (r >> 4) & 3, mr = r & 15;
+                    sb[((wmr * 16 + mr) * NB + blk) * 4 + mt] = (uint8_t)(v[k >> 2] >> (8 * (k & 3)));
+                }
+            }
+        }
+    }
+
+    // A: this lane's rows (4 tiles of 16) and its block within each k-step
+    uint32_t aoff[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+        aoff[mt] = (uint32_t)(row0 + wm * 64 + mt * 16 + m) * row_bytes + (uint32_t)g * 16u;
+    // B: this thread's staging units: token rows r = tid/16 + 32u (u < 4), chunk c = tid%16
+    const int bc = threadIdx.x & 15;
+    uint32_t boff[kG2BUnits];
+#pragma unroll
+    for (int u = 0; u < kG2BUnits; ++u) {
+        const int r = (threadIdx.x >> 4) + 32 * u;
+        const int q = min(tok0 + r, ne - 1);  // rows past the expert's tokens: any valid row
+        const uint32_t arow_act = (MODE == kModeGateUp) ? (uint32_t)(p.perm[p0 + q] / p.top_k) : (uint32_t)(p0 + q);
+        boff[u] = arow_act * (uint32_t)(p.Kdim * 2) + (uint32_t)bc * 16u;
+    }
+    constexpr uint32_t kPast = 0x80000000u;  // offset past every range: zeros
+    auto load_a = [&](int ks, u32x4_t (&a)[4]) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+            a[mt] = gemm_load16(rw, (ks * 4 + g < NB) ? aoff[mt] + (uint32_t)ks * 64u : kPast);  // ks >= nks: false
+    };
+    auto load_b = [&](int ks, u32x4_t (&b)[kG2BUnits]) {
+        const bool ok = ks * kKS + bc * 8 < p.Kdim;  // per lane (a uniform test would become a branch)
+#pragma unroll
+        for (int u = 0; u < kG2BUnits; ++u) b[u] = gemm_load16(ract, ok ? boff[u] + (uint32_t)ks * (kKS * 2) : kPast);
+    };
+    auto store_b = [&](int buf, const u32x4_t (&b)[kG2BUnits]) {
+        u32x4_t* bs = (u32x4_t*)bsm + buf * (kTN * kG2BRow);
+#pragma unroll
+        for (int u = 0; u < kG2BUnits; ++u) bs[((threadIdx.x >> 4) + 32 * u) * kG2BRow + bc] = b[u];
+    };
+
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // prologue: A for steps 0, 1; B for step 0 into LDS, B for step 1 in registers.
+    // Rings: A[ks % 3] holds step ks, Bv[ks % 2] step ks (before it is stored)
+    // or ks + 2 (after). Six steps are unrolled so that every ring index is a
+    // constant: no register copies, whose sources would have to be waited for.
+    u32x4_t A[3][4];
+    u32x4_t Bv[2][kG2BUnits];
+    load_a(0, A[0]);
+    load_b(0, Bv[0]);
+    load_a(1, A[1]);
+    load_b(1, Bv[1]);
+    store_b(0, Bv[0]);
+    __syncthreads();  // B(0) and the scales are in LDS
+    for (int kb = 0; kb < nks; kb += 6) {
+#pragma unroll
+        for (int u = 0; u < 6; ++u) {
+            const int ks = kb + u;
+            // loads for step ks + 2 go out first (past K: zeros, no traffic), always,
+            // so that the rings never hold either-or values
+            load_a(ks + 2, A[(u + 2) % 3]);
+            load_b(ks + 2, Bv[u % 2]);
+            if (ks < nks) {  // block-uniform
+                const uint4* bs = lds + (ks & 1) * (kTN * kG2BRow);
+                if (wave_rows) {
+                    const bool in = ks * 4 + g < NB;
+                    const uint32_t s4 = in ? ssm[(wm * 16 + m) * NB + ks * 4 + g] : 0u;
+                    uint32_t sc[4];
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) sc[mt] = (s4 >> (8 * mt)) & 0xffu;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        uint4 b[4];
+#pragma unroll
+                        for (int nt = 0; nt < 4; ++nt) b[nt] = bs[(wn * 64 + nt * 16 + m) * kG2BRow + g * 4 + i];
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) {
+                            const bf16x8_t a = mx_cvt8(A[u % 3][mt][i], e8m0_scale_operand(sc[mt]));
+#pragma unroll
+                            for (int nt = 0; nt < 4; ++nt)
+                                acc[mt][nt] = mfma16x16x32(a, as_bf16x8(b[nt]), acc[mt][nt]);
+                        }
+                    }
+                }
+                // B of step ks + 1 (loaded during step ks - 1) into the other buffer
+                if (ks + 1 < nks) store_b((ks + 1) & 1, Bv[(u + 1) % 2]);
+                __syncthreads();
+            }
+        }
+    }
+
+    // ---- epilogue ----
+    if (!wave_rows) return;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        const int q = tok0 + wn * 64 + nt * 16 + m;  // token column of this lane
+        if (q >= ne) continue;
+        const int pp = p0 + q;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const int rr = row0 + wm * 64 + mt * 16 + 4 * g;
+            if (rr >= p.R) continue;
+            float bsum[4] = {0.f, 0.f, 0.f, 0.f};
+            if (p.bias) {
+                const uint2 bb = *(const uint2*)(p.bias + (size_t)e * p.R + rr);
+                bsum[0] = bf16_lo(bb.x);
+                bsum[1] = bf16_hi(bb.x);
+                bsum[2] = bf16_lo(bb.y);
+                bsum[3] = bf16_hi(bb.y);
+            }
+            const f32x4_t c = acc[mt][nt];
+            if (MODE == kModeGateUp) {
+                const float h0 = swiglu(c[0] + bsum[0], c[1] + bsum[1], p.alpha, p.limit);
+                const float h1 = swiglu(c[2] + bsum[2], c[3] + bsum[3], p.alpha, p.limit);
+                const int I = p.R >> 1;
+                uint32_t* hout = (uint32_t*)((uint16_t*)p.out + (size_t)pp * I + (rr >> 1));
+                *hout = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
+            } else {
+                float4 y;
+                y.x = c[0] + bsum[0];
+                y.y = c[1] + bsum[1];
+                y.z = c[2] + bsum[2];
+                y.w = c[3] + bsum[3];
+                *(float4*)((float*)p.out + (size_t)pp * p.R + rr) = y;
+            }
+        }
+    }
+}
+
 int gemm_launch(int mode, const GemvParams& p, const int32_t* tprefix, int max_slots, int n_pairs,
                 hipStream_t stream) {
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)k_mx_gemm<kModeGateUp>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  160 * 1024);
-        (void)hipFuncSetAttribute((const void*)k_mx_gemm<kModeDown>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  160 * 1024);
+        const void* ks[] = {(const void*)k_mx_gemm<kModeGateUp>, (const void*)k_mx_gemm<kModeDown>,
+                            (const void*)k_mx_gemm2<kModeGateUp>, (const void*)k_mx_gemm2<kModeDown>};
+        for (const void* k : ks) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr_set = true;
     }
     if (p.split != 1) return set_error(PHYSLLM_MOE_EINVAL, "gemm: split must be 1");
+    const long token_tiles_ub = (long)(n_pairs + kTN - 1) / kTN + max_slots;
+    if ((p.Kdim >> 5) <= kG2MaxNB) {
+        // wide tiles; the tile's scales are staged in LDS
+        long tiles = (long)((p.R + kG2TM - 1) / kG2TM) * token_tiles_ub;
+        tiles = (tiles + 7) & ~7L;
+        if (tiles > 0x7fffffffL) return set_error(PHYSLLM_MOE_EINVAL, "gemm: too many tiles");
+        const size_t lds = (size_t)2 * kTN * kG2BRow * 16 + (size_t)kG2TM * kG2MaxNB;  // B tiles, scales
+        if (mode == kModeGateUp)
+            hipLaunchKernelGGL(k_mx_gemm2<kModeGateUp>, dim3((unsigned)tiles), dim3(kG2Threads), lds, stream, p,
+                               tprefix);
+        else
+            hipLaunchKernelGGL(k_mx_gemm2<kModeDown>, dim3((unsigned)tiles), dim3(kG2Threads), lds, stream, p,
+                               tprefix);
+        return check_launch(mode == kModeGateUp ? "gate_up gemm" : "down gemm");
+    }
     const int row_tiles = (p.R + kTM - 1) / kTM;
     // upper bound on token tiles: every touched expert may add one partial tile
     const long token_tiles = (long)(n_pairs + kTN - 1) / kTN + max_slots;

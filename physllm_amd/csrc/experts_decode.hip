@@ -372,7 +372,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p) {
 
 // ---------------------------------------------------------------------------
 // Streaming form (decode with many touched experts). One 8-wave workgroup per
-// CU walks a contiguous range of work items (pass-table entry, K split, 128-row
+// CU walks a round-robin share of work items (pass-table entry, K split, 128-row
 // set): at most 16 tokens of one expert against 128 weight rows; wave w owns
 // rows 16w..16w+15 of the set. The 23 weight stripes of a tile sit in a
 // circular register buffer: right after k-step j of the current item has been
@@ -438,9 +438,13 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
     const int per = (NB + p.split - 1) / p.split;  // <= 92 and NB <= 96: checked by the launcher
     const int sets = (p.R + kSetRows - 1) / kSetRows;
     const int total = *n_passes * p.split * sets;
-    const int f0 = (int)((long)total * blockIdx.x / gridDim.x);
-    const int f1 = (int)((long)total * (blockIdx.x + 1) / gridDim.x);
-    if (f0 >= f1) return;
+    // round-robin items, XCD-aware: workgroup b (XCD b % 8) takes items i(b) + k * G
+    // with i(b) = (b % 8) * (G / 8) + b / 8, so items next to each other in the
+    // order (the chunks of one weight tile, the row sets of one expert) run at the
+    // same time on one XCD and share its L2
+    const int G = gridDim.x;  // a multiple of 8
+    const int f0 = (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3), fstep = G;
+    if (f0 >= total) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int m = lane & 15, g = lane >> 4;
@@ -518,9 +522,9 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
     act_store(cur);
     int buf = 0;
 
-    for (int f = f0; f < f1; ++f) {
-        const bool has_next = f + 1 < f1;
-        const StreamItem nxt = stream_item(p, passes, has_next ? f + 1 : f, sets, per, NB, wave);
+    for (int f = f0; f < total; f += fstep) {
+        const bool has_next = f + fstep < total;
+        const StreamItem nxt = stream_item(p, passes, has_next ? f + fstep : f, sets, per, NB, wave);
         const bool restage = has_next && nxt.key != cur.key;
         side_load(nxt, restage);
         const __amdgpu_buffer_rsrc_t rsrc = wrsrc(nxt, has_next);
@@ -646,13 +650,15 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
     const bool stream_ok = p.split == 1 && (int64_t)p.R * (p.Kdim / 2) < 0x80000000LL;
     if (fast && stream_ok && p.passes && max_tokens > 1 && stream_items >= 2L * n_cu) {
         // many touched experts: persistent streaming kernel, one 8-wave group per CU
+        // (a multiple of 8 groups: the item order is XCD-aware)
+        const unsigned grid = (unsigned)((n_cu + 7) & ~7);
         const size_t lds = (size_t)kPassRows * (4 * per + 1) * 16 + (size_t)2 * kStreamWaves * 16 * 96;
         p.rt = 1;
         if (mode == kModeGateUp)
-            hipLaunchKernelGGL(k_mx_gemv_stream<kModeGateUp>, dim3(n_cu), dim3(kStreamThreads), lds, stream, p,
+            hipLaunchKernelGGL(k_mx_gemv_stream<kModeGateUp>, dim3(grid), dim3(kStreamThreads), lds, stream, p,
                                p.passes, p.perm, p.n_passes, p.out);
         else
-            hipLaunchKernelGGL(k_mx_gemv_stream<kModeDown>, dim3(n_cu), dim3(kStreamThreads), lds, stream, p,
+            hipLaunchKernelGGL(k_mx_gemv_stream<kModeDown>, dim3(grid), dim3(kStreamThreads), lds, stream, p,
                                p.passes, p.perm, p.n_passes, p.out);
     } else if (fast) {
         // activation units one thread stages per pass: ntok rows x 4*per 16-byte units

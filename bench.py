@@ -30,15 +30,15 @@ METRIC = "MoE-layer tokens/sec + % HBM peak (decode) / % MFMA peak (prefill), 1 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
 
 
-def measured_traffic(cfg_index: int):
-    """HBM bytes per launch of the gate_up kernel from the committed rocprofv3 --pmc
+def measured_traffic(cfg_index: int, kernel: str = "gate_up"):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc
     summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration)."""
     import re
     try:
         text = open(TRAFFIC_SUMMARY).read()
     except OSError:
         return None
-    m = re.search(r"^traffic\[config%d\.gate_up\]\s*=\s*(\d+)" % cfg_index, text, re.M)
+    m = re.search(r"^traffic\[config%d\.%s\]\s*=\s*(\d+)" % (cfg_index, kernel), text, re.M)
     return int(m.group(1)) if m else None
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=[0, 2, 3, 4])
+    ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3, 4])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -88,6 +88,9 @@ def main():
     from physllm_amd import synthetic as syn
 
     cfg_i = args.config
+    if cfg_i == 1:
+        bench_dequant(args)
+        return
     cfgd = syn.CONFIGS[cfg_i]
     log(f"[bench] generating config {cfg_i}: {cfgd['workload']}")
     layer, x = syn.make_config(cfg_i)
@@ -257,6 +260,88 @@ def main():
                   "wall_s_timed_region": round(wall, 4),
                   "launch": "hip graph replay" if args.graph else "eager C-ABI call per step",
                   "eager_ms_per_step": round(eager_ms, 5)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+def bench_dequant(args):
+    """Config 1: standalone MXFP4 -> bf16 dequant of a [32, 5760, 2880] tensor through
+    physllm_moe_mxfp4_dequant. A step is one whole-tensor launch; the 1.34 GB it moves
+    is five times the Infinity Cache, so no rotation is needed. Value = algorithmic
+    bytes (codes + scales read, bf16 written) per second."""
+    import torch
+    from physllm_amd import ops
+    from physllm_amd import synthetic as syn
+
+    cfgd = syn.CONFIGS[1]
+    log(f"[bench] generating config 1: {cfgd['workload']}")
+    packed, scales, numel = syn.make_dequant_input()
+    pd = torch.from_numpy(packed).cuda()
+    sd = torch.from_numpy(scales).cuda()
+    out = torch.empty(numel, dtype=torch.int16, device="cuda")
+    stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
+    alg = numel // 2 + numel // 32 + 2 * numel
+
+    for _ in range(args.warmup):
+        ops.mxfp4_dequant(pd, sd, out, s)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        ops.mxfp4_dequant(pd, sd, out, s)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = ev0.elapsed_time(ev1) / args.steps
+    gbs = alg / (ms * 1e-3) / 1e9
+
+    # spot check: one expert's slab against the oracle (bit-exact)
+    from oracle import oracle as orc
+    per = 5760 * 2880
+    e = 17
+    got = out[e * per:(e + 1) * per].cpu().numpy().view(np.uint16)
+    exp = orc.mxfp4_dequant(packed[e * per // 2:(e + 1) * per // 2], scales[e * per // 32:(e + 1) * per // 32], per)
+    assert np.array_equal(got, exp), "dequant output differs from the oracle"
+
+    cpu = None
+    if not args.no_cpu:
+        nthr = orc.default_threads()
+        n, tcpu = 0, 0.0
+        while tcpu < args.cpu_seconds and n < 4096:
+            e = n % 32
+            sl = slice(e * per // 2, (e + 1) * per // 2)
+            ss = slice(e * per // 32, (e + 1) * per // 32)
+            t1 = time.perf_counter()
+            orc.mxfp4_dequant(packed[sl], scales[ss], per, nthreads=nthr)
+            tcpu += time.perf_counter() - t1
+            n += 1
+        cpu = {"value": round(n * (per // 2 + per // 32 + 2 * per) / tcpu / 1e9, 3), "unit": "GB/s",
+               "cores": nthr, "kind": "port",
+               "sample": f"{n} expert slabs [5760,2880] (cycling over the 32) through the oracle's "
+                         f"dequant ({tcpu:.1f} s, OpenMP over blocks)"}
+
+    res = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8->bf16",
+        "data": "synthetic (seeded; e2m1 codes uniform 0-15, E8M0 scales 2^-8..2^-4)",
+        "config": {"workload": cfgd["workload"], "config_index": 1, "numel": numel,
+                   "bytes_algorithmic": alg},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(1, "dequant"),
+                     "kernel": "k_mxfp4_dequant32", "work_per_launch": alg},
+        "layer": {"wall_s_timed_region": round(wall, 4), "launch": "eager C-ABI call per step"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)

@@ -221,17 +221,12 @@ constexpr int kG2Threads = 512;
 constexpr int kG2TM = 256;
 constexpr int kG2BUnits = kTN * (kKS * 2 / 16) / kG2Threads;  // 4 B units per thread per k-step
 constexpr int kG2MaxNB = 96;                                   // scale row bytes staged per tile row
-constexpr int kG2BRow = kBRowU;                                // LDS row stride of the B tile (16-byte units)
+constexpr int kG2BRow = kKS * 2 / 16;  // B tile row (one token's k-step): 16 units of 16 bytes, XOR-swizzled
 
+// One 256-row x 128-token tile t of the wide-tile GEMM.
 template <int MODE>
-__global__ __launch_bounds__(kG2Threads, 1) void k_mx_gemm2(GemvParams p, const int32_t* __restrict__ tprefix) {
-    extern __shared__ uint4 lds[];
-    const int G = gridDim.x;  // a multiple of 8
-    const int bid = blockIdx.x;
-    const int t = (bid & 7) * (G >> 3) + (bid >> 3);
-    const int n_slots = *p.n_slots;
-    const int row_tiles = (p.R + kG2TM - 1) / kG2TM;
-    if (t >= row_tiles * tprefix[n_slots]) return;
+__device__ __forceinline__ void mx_gemm2_tile(const GemvParams& p, const int32_t* __restrict__ tprefix, int t,
+                                              int row_tiles, int n_slots, uint4* lds) {
     int lo = 0, hi = n_slots;  // largest s with row_tiles * tprefix[s] <= t
     while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
@@ -255,42 +250,32 @@ __global__ __launch_bounds__(kG2Threads, 1) void k_mx_gemm2(GemvParams p, const 
     const int nks = (NB + 3) >> 2;
     const uint32_t row_bytes = (uint32_t)(p.Kdim >> 1);
     const uint32_t exp_w = (uint32_t)p.R * row_bytes;
-    const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;
-    const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(p.blocks + (size_t)e * exp_w, exp_w);
-    const __amdgpu_buffer_rsrc_t rsc = gemm_rsrc(p.scales + (size_t)e * exp_s, exp_s);
-    const __amdgpu_buffer_rsrc_t ract = gemm_rsrc(p.act, (uint32_t)p.act_rows * (uint32_t)p.Kdim * 2u);
+    const uint32_t act_bytes = (uint32_t)p.act_rows * (uint32_t)p.Kdim * 2u;
+    const uint8_t* wexp = p.blocks + (size_t)e * exp_w;
 
-    uint4* bsm = lds;                                        // [2][kTN][kG2BRow]
-    // scales of the tile's rows, all of K, as [4 row blocks wm][16 rows m][NB][4 tiles mt]:
-    // the 4 scales a lane needs for one block are one dword
-    uint32_t* ssm = (uint32_t*)(lds + 2 * kTN * kG2BRow);
-
-    // ---- stage the scales: 16-byte global loads of the 256 x NB bytes, scattered
-    // byte by byte into the transposed layout ----
+    // B tile [2][kTN][16 units]: unit c of token row r sits at r * 16 + (c ^ (r & 15)), so the
+    // 16 token rows of a fragment read (same c, rows r0..r0+15) cover all 64 banks
+    uint4* bsm = lds;
+    // the tile's scales, row-major [256][NB] as in memory (rows past R: zeros)
+    uint8_t* ssm = (uint8_t*)(lds + 2 * kTN * kG2BRow);
     {
-        const int nunits = (kG2TM * NB + 15) / 16;
-        const uint32_t sbase = (uint32_t)row0 * NB;
-        uint8_t* sb = (uint8_t*)ssm;
-        for (int u = threadIdx.x; u < nunits; u += kG2Threads) {
-            const u32x4_t v = gemm_load16(rsc, sbase + 16u * u);  // rows past R read zeros
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int idx = 16 * u + k;  // byte of the tile: row r = idx / NB, block idx % NB
-                if (idx < kG2TM * NB) {
-                    const int r = idx / NB, blk = idx - r * NB;
-                    const int wmr = r >> 6, mt = (r >> 4) & 3, mr = r & 15;
-                    sb[((wmr * 16 + mr) * NB + blk) * 4 + mt] = (uint8_t)(v[k >> 2] >> (8 * (k & 3)));
-                }
-            }
-        }
+        const int rows = min(kG2TM, p.R - row0);
+        const __amdgpu_buffer_rsrc_t rsc =
+            gemm_rsrc(p.scales + ((size_t)e * p.R + row0) * NB, (uint32_t)rows * (uint32_t)NB);
+        const int nunits = (kG2TM * NB) >> 4;  // 256 * NB is a multiple of 16
+        for (int u = threadIdx.x; u < nunits; u += kG2Threads)
+            ((u32x4_t*)ssm)[u] = gemm_load16(rsc, 16u * (uint32_t)u);
     }
 
-    // A: this lane's rows (4 tiles of 16) and its block within each k-step
+    // A: this lane's 4 rows (one per 16-row tile) at block g of a k-step; rows past
+    // R lie past the buffer range and read zeros. The buffer base advances by one
+    // k-step (64 bytes of every row) per step in scalar registers, so the lane
+    // offsets never change.
     uint32_t aoff[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
         aoff[mt] = (uint32_t)(row0 + wm * 64 + mt * 16 + m) * row_bytes + (uint32_t)g * 16u;
-    // B: this thread's staging units: token rows r = tid/16 + 32u (u < 4), chunk c = tid%16
+    // B: this thread's staging units: token rows r = tid/16 + 32u (u < 4), 16-byte chunk c = tid%16
     const int bc = threadIdx.x & 15;
     uint32_t boff[kG2BUnits];
 #pragma unroll
@@ -302,19 +287,27 @@ __global__ __launch_bounds__(kG2Threads, 1) void k_mx_gemm2(GemvParams p, const 
     }
     constexpr uint32_t kPast = 0x80000000u;  // offset past every range: zeros
     auto load_a = [&](int ks, u32x4_t (&a)[4]) {
+        // ks >= nks: an empty range (no traffic)
+        const uint32_t adv = (uint32_t)ks * 64u;
+        const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(wexp + adv, ks < nks ? exp_w - adv : 0u);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-            a[mt] = gemm_load16(rw, (ks * 4 + g < NB) ? aoff[mt] + (uint32_t)ks * 64u : kPast);  // ks >= nks: false
+        for (int mt = 0; mt < 4; ++mt) a[mt] = gemm_load16(rw, aoff[mt]);
     };
     auto load_b = [&](int ks, u32x4_t (&b)[kG2BUnits]) {
-        const bool ok = ks * kKS + bc * 8 < p.Kdim;  // per lane (a uniform test would become a branch)
+        // chunks past K read zeros (the next row's elements must not enter the sums)
+        const uint32_t adv = (uint32_t)ks * (kKS * 2);
+        const __amdgpu_buffer_rsrc_t ra = gemm_rsrc(p.act + adv / 2, ks < nks ? act_bytes - adv : 0u);
+        const bool ok = ks * kKS + bc * 8 < p.Kdim;
 #pragma unroll
-        for (int u = 0; u < kG2BUnits; ++u) b[u] = gemm_load16(ract, ok ? boff[u] + (uint32_t)ks * (kKS * 2) : kPast);
+        for (int u = 0; u < kG2BUnits; ++u) b[u] = gemm_load16(ra, ok ? boff[u] : kPast);
     };
     auto store_b = [&](int buf, const u32x4_t (&b)[kG2BUnits]) {
         u32x4_t* bs = (u32x4_t*)bsm + buf * (kTN * kG2BRow);
 #pragma unroll
-        for (int u = 0; u < kG2BUnits; ++u) bs[((threadIdx.x >> 4) + 32 * u) * kG2BRow + bc] = b[u];
+        for (int u = 0; u < kG2BUnits; ++u) {
+            const int r = (threadIdx.x >> 4) + 32 * u;
+            bs[r * kG2BRow + (bc ^ (r & 15))] = b[u];
+        }
     };
 
     f32x4_t acc[4][4];
@@ -322,6 +315,10 @@ __global__ __launch_bounds__(kG2Threads, 1) void k_mx_gemm2(GemvParams p, const 
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // this lane's scale bytes: row (wm*64 + mt*16 + m), block 4ks + g
+    const uint8_t* sl = ssm + (wm * 64 + m) * NB + g;
+    const uint4* bl = lds + (wn * 64 + m) * kG2BRow;  // fragment rows: r & 15 == m
 
     // prologue: A for steps 0, 1; B for step 0 into LDS, B for step 1 in registers.
     // Rings: A[ks % 3] holds step ks, Bv[ks % 2] step ks (before it is stored)
@@ -344,18 +341,23 @@ __global__ __launch_bounds__(kG2Threads, 1) void k_mx_gemm2(GemvParams p, const 
             load_a(ks + 2, A[(u + 2) % 3]);
             load_b(ks + 2, Bv[u % 2]);
             if (ks < nks) {  // block-uniform
-                const uint4* bs = lds + (ks & 1) * (kTN * kG2BRow);
                 if (wave_rows) {
-                    const bool in = ks * 4 + g < NB;
-                    const uint32_t s4 = in ? ssm[(wm * 16 + m) * NB + ks * 4 + g] : 0u;
+                    // blocks past NB (last step): scale 0, so the (finite) codes read
+                    // there cannot make a NaN against the zero activations
+                    // the reads are unconditional (in LDS bounds for every step) and the
+                    // mask is opaque, so they are not turned into masked reads that
+                    // would each be waited for on their own
+                    uint32_t keep = (4 * ks + g < NB) ? 0xffu : 0u;
+                    asm volatile("" : "+v"(keep));
                     uint32_t sc[4];
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt) sc[mt] = (s4 >> (8 * mt)) & 0xffu;
+                    for (int mt = 0; mt < 4; ++mt) sc[mt] = (uint32_t)sl[mt * 16 * NB + 4 * ks] & keep;
+                    const uint4* bs = bl + (ks & 1) * (kTN * kG2BRow);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         uint4 b[4];
 #pragma unroll
-                        for (int nt = 0; nt < 4; ++nt) b[nt] = bs[(wn * 64 + nt * 16 + m) * kG2BRow + g * 4 + i];
+                        for (int nt = 0; nt < 4; ++nt) b[nt] = bs[nt * 16 * kG2BRow + ((g * 4 + i) ^ m)];
 #pragma unroll
                         for (int mt = 0; mt < 4; ++mt) {
                             const bf16x8_t a = mx_cvt8(A[u % 3][mt][i], e8m0_scale_operand(sc[mt]));
@@ -410,6 +412,22 @@ __global__ __launch_bounds__(kG2Threads, 1) void k_mx_gemm2(GemvParams p, const 
     }
 }
 
+template <int MODE>
+__global__ __launch_bounds__(kG2Threads, 1) void k_mx_gemm2(GemvParams p, const int32_t* __restrict__ tprefix) {
+    extern __shared__ uint4 lds[];
+    // Persistent: the tiles (expert slot, row tile, token tile in that order) are
+    // split into 8 contiguous ranges, one per XCD (workgroup b runs on XCD b % 8),
+    // so every XCD gets the same number of tiles and works on few experts at a time.
+    const int n_slots = *p.n_slots;
+    const int row_tiles = (p.R + kG2TM - 1) / kG2TM;
+    const int T = row_tiles * tprefix[n_slots];
+    const int xcd = blockIdx.x & 7, per_xcd = gridDim.x >> 3;
+    const int t_end = (int)(((int64_t)(xcd + 1) * T) >> 3);
+    for (int t = (int)(((int64_t)xcd * T) >> 3) + (int)(blockIdx.x >> 3); t < t_end; t += per_xcd) {
+        mx_gemm2_tile<MODE>(p, tprefix, t, row_tiles, n_slots, lds);
+    }
+}
+
 int gemm_launch(int mode, const GemvParams& p, const int32_t* tprefix, int max_slots, int n_pairs,
                 hipStream_t stream) {
     static bool attr_set = false;
@@ -422,10 +440,18 @@ int gemm_launch(int mode, const GemvParams& p, const int32_t* tprefix, int max_s
     if (p.split != 1) return set_error(PHYSLLM_MOE_EINVAL, "gemm: split must be 1");
     const long token_tiles_ub = (long)(n_pairs + kTN - 1) / kTN + max_slots;
     if ((p.Kdim >> 5) <= kG2MaxNB) {
-        // wide tiles; the tile's scales are staged in LDS
-        long tiles = (long)((p.R + kG2TM - 1) / kG2TM) * token_tiles_ub;
-        tiles = (tiles + 7) & ~7L;
-        if (tiles > 0x7fffffffL) return set_error(PHYSLLM_MOE_EINVAL, "gemm: too many tiles");
+        // wide tiles, persistent: one workgroup per CU (a multiple of 8, one range of
+        // tiles per XCD); the tile count is only known on the device
+        const long tiles_ub = (long)((p.R + kG2TM - 1) / kG2TM) * token_tiles_ub;
+        if (tiles_ub > 0x7fffffffL) return set_error(PHYSLLM_MOE_EINVAL, "gemm: too many tiles");
+        static int n_cu = 0;
+        if (n_cu == 0) {
+            int dev = 0;
+            (void)hipGetDevice(&dev);
+            if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+                n_cu = 256;
+        }
+        const long tiles = (n_cu + 7) & ~7;
         const size_t lds = (size_t)2 * kTN * kG2BRow * 16 + (size_t)kG2TM * kG2MaxNB;  // B tiles, scales
         if (mode == kModeGateUp)
             hipLaunchKernelGGL(k_mx_gemm2<kModeGateUp>, dim3((unsigned)tiles), dim3(kG2Threads), lds, stream, p,

@@ -20,5 +20,9 @@ int dequant_launch(const void* packed, const void* scales, void* out, int64_t nu
                    hipStream_t stream);
 int router_launch(const void* x, const void* w, const void* bias, int B, int H, int E, int K, void* idx,
                   void* wts, hipStream_t stream);
+// Batch-1 route: router, top-k, softmax and bucketing in one launch (E <= 256).
+int route1_launch(const void* x, const void* w, const void* bias, int H, int E, int K, void* idx, void* wts,
+                  void* counts, void* offsets, void* perm, void* pos, void* slots, void* n_slots, void* passes,
+                  void* n_passes, hipStream_t stream);
 
 }  // namespace physllm

@@ -156,13 +156,20 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
     float* wts = topk_w ? (float*)topk_w : ws.wts;
 
     if (stages & kStageRoute) {
-        if ((rc = router_launch(x, w->router_w, w->router_b, batch, c.hidden, c.num_experts, c.top_k, idx, wts, s)))
-            return rc;
-        // prefill: the GEMM's token-tile prefix; decode: the GEMV's pass table
         const bool gemm = use_gemm(c, batch);
-        if ((rc = bucket_launch(idx, N, c.num_experts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.slots, ws.n_slots,
-                                gemm ? ws.tprefix : nullptr, kGemmTileN, gemm ? nullptr : ws.passes, ws.n_passes, s)))
-            return rc;
+        if (batch == 1 && !gemm && c.num_experts <= 256) {
+            // one token: the whole route (and the bucketing of its k pairs) in one launch
+            rc = route1_launch(x, w->router_w, w->router_b, c.hidden, c.num_experts, c.top_k, idx, wts, ws.counts,
+                               ws.offsets, ws.perm, ws.pos, ws.slots, ws.n_slots, ws.passes, ws.n_passes, s);
+        } else {
+            rc = router_launch(x, w->router_w, w->router_b, batch, c.hidden, c.num_experts, c.top_k, idx, wts, s);
+            // prefill: the GEMM's token-tile prefix; decode: the GEMV's pass table
+            if (!rc)
+                rc = bucket_launch(idx, N, c.num_experts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.slots,
+                                   ws.n_slots, gemm ? ws.tprefix : nullptr, kGemmTileN, gemm ? nullptr : ws.passes,
+                                   ws.n_passes, s);
+        }
+        if (rc) return rc;
     }
     const int max_slots = N < c.num_experts ? N : c.num_experts;
     GemvParams p{};

@@ -271,6 +271,119 @@ __global__ __launch_bounds__(kRouterThreads) void k_router(const uint16_t* __res
     }
 }
 
+// ---------------------------------------------------------------------------
+// One-token route (decode at batch 1): router logits, top-k, softmax and the
+// bucketing of the k pairs in one workgroup of 16 waves, one launch instead of
+// two. Wave w computes the logits of experts w * EPI.. (every 16-byte chunk of
+// its rows loaded up front, as k_router does); wave 0 then ranks them
+// (compute_ranks, the order of rank_beats) and, since a token's k experts are
+// distinct, the stable counting sort of its k pairs by expert is the ascending
+// order of the selected ids: pair j goes to sorted position #{i : e_i < e_j}.
+// E <= 256 (the rank scratch of one wave).
+// ---------------------------------------------------------------------------
+constexpr int kRoute1Threads = 1024;
+
+template <int EPI>
+__global__ __launch_bounds__(kRoute1Threads) void k_route1(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias, int H, int E,
+    int K, int32_t* __restrict__ idx, float* __restrict__ wts, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ pos, int4* __restrict__ slots,
+    int32_t* __restrict__ n_slots, int4* __restrict__ passes, int32_t* __restrict__ n_passes, int vec) {
+    extern __shared__ double lg[];  // [E] logits | rank scratch | selected ids [32], values [32]
+    constexpr int NW = kRoute1Threads / 64;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int e0 = wave * EPI; e0 < E; e0 += NW * EPI) {
+        double acc[EPI][1];
+        if (vec) {
+            router_dots<1, EPI, 6>(x, w, 0, 1, e0, E, H, lane, acc);
+        } else {
+#pragma unroll
+            for (int ei = 0; ei < EPI; ++ei) acc[ei][0] = 0.0;
+            for (int d = lane; d < H; d += 64) {
+                const float xv = bf16_to_f32(x[d]);
+#pragma unroll
+                for (int ei = 0; ei < EPI; ++ei)
+                    if (e0 + ei < E) acc[ei][0] = acc_prod(acc[ei][0], xv, bf16_to_f32(w[(size_t)(e0 + ei) * H + d]));
+            }
+        }
+#pragma unroll
+        for (int ei = 0; ei < EPI; ++ei) {
+            const int e = e0 + ei;
+            const double b = (bias && e < E) ? (double)bf16_to_f32(bias[e]) : 0.0;
+            const double sum = wave_sum_f64(acc[ei][0]);
+            if (lane == 0 && e < E) lg[e] = sum + b;
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+
+    void* scratch = (void*)(lg + E);
+    int32_t* selid = (int32_t*)((char*)scratch + kRankScratchBytes);
+    double* selval = (double*)(selid + 32);
+    double vals[4];
+    int ids[4], rank[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ids[i] = lane + 64 * i;
+        vals[i] = ids[i] < E ? lg[ids[i]] : 0.0;
+    }
+    compute_ranks(vals, ids, E, lane, scratch, rank);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (ids[i] < E && rank[i] < K) {
+            selid[rank[i]] = ids[i];
+            selval[rank[i]] = vals[i];
+        }
+    __builtin_amdgcn_wave_barrier();
+    const int ej = lane < K ? selid[lane] : 0x7fffffff;  // pair j = lane (token 0, slot j)
+    const double vj = lane < K ? selval[lane] : 0.0;
+    // softmax over the k selected in selection order (the first pick is the maximum)
+    const double ex = lane < K ? exp(vj - selval[0]) : 0.0;
+    double sum = 0.0;
+    for (int j = 0; j < K; ++j) sum += __shfl(ex, j, 64);
+    // sorted position of pair j: the number of selected experts below e_j
+    int pj = 0;
+    for (int i = 0; i < K; ++i) pj += (__shfl(ej, i, 64) < ej) ? 1 : 0;
+    if (lane < K) {
+        idx[lane] = ej;
+        wts[lane] = (float)(ex / sum);
+        pos[lane] = pj;
+        perm[pj] = lane;
+        slots[pj] = make_int4(ej, 1, pj, 0);
+        passes[pj] = make_int4(ej, 1, pj, 1 << 16);
+    }
+    if (lane == 0) {
+        *n_slots = K;
+        *n_passes = K;
+        offsets[E] = K;
+    }
+    // counts[e] = 1 for the selected experts, offsets[e] = #{selected < e}; later slots cleared
+    for (int e = lane; e < E; e += 64) {
+        int c = 0, below = 0;
+        for (int i = 0; i < K; ++i) {
+            const int ei = __shfl(ej, i, 64);
+            c += (ei == e) ? 1 : 0;
+            below += (ei < e) ? 1 : 0;
+        }
+        counts[e] = c;
+        offsets[e] = below;
+        if (e >= K) slots[e] = make_int4(0, 0, 0, 0);
+    }
+}
+
+int route1_launch(const void* x, const void* w, const void* bias, int H, int E, int K, void* idx, void* wts,
+                  void* counts, void* offsets, void* perm, void* pos, void* slots, void* n_slots, void* passes,
+                  void* n_passes, hipStream_t stream) {
+    if (E > kRankMax || K > E || K > kMaxTopK) return set_error(PHYSLLM_MOE_EINVAL, "route1: sizes out of range");
+    const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0);
+    const size_t lds = (size_t)E * sizeof(double) + kRankScratchBytes + 32 * 4 + 32 * 8;
+    hipLaunchKernelGGL((k_route1<2>), dim3(1), dim3(kRoute1Threads), lds, stream, (const uint16_t*)x,
+                       (const uint16_t*)w, (const uint16_t*)bias, H, E, K, (int32_t*)idx, (float*)wts,
+                       (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm, (int32_t*)pos, (int4*)slots,
+                       (int32_t*)n_slots, (int4*)passes, (int32_t*)n_passes, vec);
+    return check_launch("route1");
+}
+
 int router_launch(const void* x, const void* w, const void* bias, int B, int H, int E, int K, void* idx,
                   void* wts, hipStream_t stream) {
     if (B < 0 || H < 1 || E < 1 || K < 1) return set_error(PHYSLLM_MOE_EINVAL, "router: bad sizes");

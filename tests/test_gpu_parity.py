@@ -280,6 +280,40 @@ def test_layer_streaming_gemv(oracle, E, H, I, K, B, hot, bias):
     _check_layer(oracle, layer, x, f"stream E={E} H={H} I={I} K={K} B={B} hot={hot} bias={bias}")
 
 
+@pytest.mark.parametrize("E,H,I,K", [(32, 2880, 2880, 4), (256, 256, 128, 8), (128, 4096, 256, 4),
+                                     (4, 64, 64, 4), (7, 96, 64, 1)])
+def test_layer_batch1_fused_route(oracle, E, H, I, K):
+    """Batch 1 routes in one launch (router, top-k, softmax and the bucketing of the
+    token's k pairs): E up to the 256 limit, k = E, k = 1, a hidden size needing
+    two passes of the row loads (4096)."""
+    layer = syn.make_layer(E, H, I, K, seed=E * 3 + K)
+    x = syn.make_x(1, H, seed=E + H)
+    _check_layer(oracle, layer, x, f"batch-1 route E={E} H={H} I={I} K={K}")
+
+
+def test_layer_batch1_route_ties_and_nan(oracle):
+    """Batch-1 route with three equal leading logits (ties go to the lower index)
+    and with a NaN activation (every logit NaN: NaN ranks lowest, so the first k
+    experts by index, as the oracle selects)."""
+    E, H, I, K = 16, 128, 64, 4
+    layer = syn.make_layer(E, H, I, K, seed=21)
+    rw = layer.router_w.copy()
+    rw[[9, 2, 5]] = rw[2]
+    rb = syn.bf16_to_f32(layer.router_b).copy()
+    rb[[2, 5, 9]] = 20.0
+    layer.router_w, layer.router_b = rw, syn.bf16_from_f32(rb)
+    x = syn.make_x(1, H, seed=21)
+    got, gidx, _, _ = _run_layer(layer, x)
+    assert gidx[0, :3].tolist() == [2, 5, 9]
+    _check_layer(oracle, layer, x, "batch-1 ties")
+    xn = x.copy()
+    xn[0, 7] = 0x7FC0
+    _, nidx, nw, _ = _run_layer(layer, xn)
+    r = oracle.moe_layer(layer, xn)
+    assert np.array_equal(nidx, r["idx"]) and nidx[0].tolist() == [0, 1, 2, 3]
+    assert np.array_equal(np.isnan(nw), np.isnan(r["wts"]))
+
+
 def test_layer_without_biases(oracle):
     layer = syn.make_layer(8, 128, 64, 2, seed=4, with_bias=False)
     x = syn.make_x(9, 128, seed=4)

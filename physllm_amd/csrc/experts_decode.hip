@@ -389,6 +389,7 @@ constexpr int kStreamWaves = 8;
 constexpr int kStreamThreads = 64 * kStreamWaves;
 constexpr int kSetRows = 16 * kStreamWaves;
 constexpr int kStreamRowLoads = 6;  // 64-unit loads per staged row: K ranges of <= 384 units (96 blocks)
+constexpr int kStreamRowStride = 64 * kStreamRowLoads + 1;  // LDS row stride of the staged activations
 constexpr int kStreamMaxNB = 96;    // a tile's scales (16 x NB bytes) fit a wave's 1536-byte slice
 
 struct StreamItem {
@@ -424,6 +425,37 @@ __device__ __forceinline__ StreamItem stream_item(const GemvParams& p, const int
     return it;
 }
 
+// The k-steps of one item in the 16-token streaming GEMV: decode k-step j of the
+// tile in wq[j] against the staged activations, then load k-step j of the next
+// item's tile into wq[j] right after its last read.
+__device__ __forceinline__ void stream_steps(u32x4_t (&wq)[kGemvNit], f32x4_t& acc0, f32x4_t& acc1, f32x4_t& acc2,
+                                             f32x4_t& acc3, const uint8_t* sl, const uint4* xl, int nblk, int g,
+                                             __amdgpu_buffer_rsrc_t rsrc, uint32_t svoff) {
+#pragma unroll
+    for (int j = 0; j < kGemvNit; ++j) {
+        if (4 * j < nblk) {  // wave-uniform
+            const bool edge = 4 * j + 3 >= nblk;
+            const bool bv = 4 * j + g < nblk;
+            uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
+            asm volatile("" : "+v"(sj));
+            const float sf = e8m0_scale_operand(sj);
+            u32x4_t q = wq[j];
+            uint4 x0 = xl[16 * j + 0], x1 = xl[16 * j + 1], x2 = xl[16 * j + 2], x3 = xl[16 * j + 3];
+            if (edge && !bv) {
+                q = u32x4_t{0u, 0u, 0u, 0u};
+                x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
+            }
+            acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
+            acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
+            acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
+            acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
+        }
+        // refill after the last read of wq[j]: the load reuses its registers
+        wq[j] = buf_load16(rsrc, svoff, 64 * j);
+        __builtin_amdgcn_sched_barrier(0);  // one refill per k-step
+    }
+}
+
 // The pass table, sorted pair ids and outputs come in as restrict kernel
 // arguments: the output stores then provably leave the tables alone and the
 // per-item table reads compile to scalar loads, which a wave does not have to
@@ -448,7 +480,9 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int m = lane & 15, g = lane >> 4;
-    const int su = 4 * per + 1;  // LDS activation row stride (16-byte units, one-unit pad)
+    // LDS activation row stride in 16-byte units: every staged row holds all 6 x 64 units a
+    // thread loads (units past the K range are never read), plus one unit of pad (odd stride)
+    const int su = kStreamRowStride;
     const uint32_t row_bytes = (uint32_t)(p.Kdim >> 1);
     const uint32_t exp_w = (uint32_t)p.R * row_bytes;
     const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;
@@ -486,17 +520,15 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
         if (lane < NB) ((u32x4_t*)s)[lane] = sv0;
         if (lane + 64 < NB) ((u32x4_t*)s)[lane + 64] = sv1;
     };
-    auto act_store = [&](const StreamItem& it) {
+    // unconditional stores: rows past the item's tokens repeat its last row and units
+    // past its K range hold the next row's elements, and neither is ever read
+    auto act_store = [&]() {
         __syncthreads();  // every wave has finished reading the previous activations
-        const int cu = 4 * it.nblk;
 #pragma unroll
         for (int r2 = 0; r2 < 2; ++r2) {
             const int r = 2 * wave + r2;
-            if (r < it.ne) {
 #pragma unroll
-                for (int u = 0; u < kStreamRowLoads; ++u)
-                    if (lane + 64 * u < cu) ((u32x4_t*)xs)[r * su + lane + 64 * u] = av[r2][u];
-            }
+            for (int u = 0; u < kStreamRowLoads; ++u) ((u32x4_t*)xs)[r * su + lane + 64 * u] = av[r2][u];
         }
         __syncthreads();
     };
@@ -519,7 +551,7 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
     side_load(cur, true);
     uint2 bcur = bnx;
     scale_store(0);
-    act_store(cur);
+    act_store();
     int buf = 0;
 
     for (int f = f0; f < total; f += fstep) {
@@ -532,29 +564,7 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
         const uint8_t* sl = scl0 + buf * kSclBuf + m * NB + cur.kb0 + g;
         const uint4* xl = xs + min(m, cur.ne - 1) * su + 4 * g;
         f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
-#pragma unroll
-        for (int j = 0; j < kGemvNit; ++j) {
-            if (4 * j < cur.nblk) {  // wave-uniform
-                const bool edge = 4 * j + 3 >= cur.nblk;
-                const bool bv = 4 * j + g < cur.nblk;
-                uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
-                asm volatile("" : "+v"(sj));
-                const float sf = e8m0_scale_operand(sj);
-                u32x4_t q = wq[j];
-                uint4 x0 = xl[16 * j + 0], x1 = xl[16 * j + 1], x2 = xl[16 * j + 2], x3 = xl[16 * j + 3];
-                if (edge && !bv) {
-                    q = u32x4_t{0u, 0u, 0u, 0u};
-                    x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
-                }
-                acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
-                acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
-                acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
-                acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
-            }
-            // refill after the last read of wq[j]: the load reuses its registers
-            wq[j] = buf_load16(rsrc, svoff, 64 * j);
-            __builtin_amdgcn_sched_barrier(0);  // one refill per k-step
-        }
+        stream_steps(wq, acc0, acc1, acc2, acc3, sl, xl, cur.nblk, g, rsrc, svoff);
         if (cur.r0 < p.R && m < cur.ne) {
             const f32x4_t acc = (acc0 + acc1) + (acc2 + acc3);
             const int pp = cur.p0 + m;
@@ -580,7 +590,7 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
         buf ^= 1;
         scale_store(buf);
         bcur = bnx;
-        if (restage) act_store(nxt);
+        if (restage) act_store();
         cur = nxt;
     }
 }
@@ -652,7 +662,7 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
         // many touched experts: persistent streaming kernel, one 8-wave group per CU
         // (a multiple of 8 groups: the item order is XCD-aware)
         const unsigned grid = (unsigned)((n_cu + 7) & ~7);
-        const size_t lds = (size_t)kPassRows * (4 * per + 1) * 16 + (size_t)2 * kStreamWaves * 16 * 96;
+        const size_t lds = (size_t)kPassRows * kStreamRowStride * 16 + (size_t)2 * kStreamWaves * 16 * 96;
         p.rt = 1;
         if (mode == kModeGateUp)
             hipLaunchKernelGGL(k_mx_gemv_stream<kModeGateUp>, dim3(grid), dim3(kStreamThreads), lds, stream, p,

@@ -210,13 +210,14 @@ def main():
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / BF16_MFMA_PEAK_TFLOPS, 4),
                 "traffic": measured_traffic(cfg_i),
-                "kernel": "gate_up grouped GEMM (k_mx_gemm<0>)", "work_per_launch": flops}
+                "kernel": "gate_up grouped GEMM (k_mx_gemm2<0>)", "work_per_launch": flops}
     else:
         alg = e_touched * gu_expert_bytes + B * H * 2 + B * K * I * 2
         achieved = alg / (gate_up_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(cfg_i),
-                "kernel": "gate_up grouped GEMV (k_mx_gemv<0,NS>)", "work_per_launch": alg}
+                "kernel": "gate_up grouped GEMV (%s)" % ("k_mx_gemv<0,2>" if B == 1 else "k_mx_gemv_stream<0>"),
+                "work_per_launch": alg}
 
     # ---- CPU baseline (oracle on this host's cores, bounded sample) ----------------------
     cpu = None

@@ -13,9 +13,10 @@
 // Layout: one workgroup of 8 waves handles TB tokens. Wave w computes experts
 // w*EPI.., with every lane's 16-byte chunks of all EPI router rows and TB token
 // rows loaded up front (a wave reads contiguous 1 KiB slices of each row), then a
-// DPP/permlane reduction per dot. Logits go to LDS; then one wave per token ranks
-// them (rank_select: one pass of broadcast LDS reads instead of k dependent
-// arg-max rounds) and writes the selection and its softmax.
+// DPP/permlane reduction per dot. Logits go to LDS; then every wave ranks a share
+// of each token's experts (ballot_select: one ballot per expert instead of k
+// dependent arg-max rounds) and one wave per token writes the selection and its
+// softmax.
 #include "common.h"
 #include "capi_internal.h"
 #include "experts.h"
@@ -83,63 +84,56 @@ __device__ __forceinline__ uint64_t order_key(double v) {
     return (b >> 63) ? ~b : (b | (1ull << 63));
 }
 
-// Per-wave LDS scratch of rank_select: keys [256], ids [256], values [2][32].
+// Largest expert count of the ballot selection (4 comparator keys per lane).
 constexpr int kRankMax = 256;
-constexpr size_t kRankScratchBytes = kRankMax * 8 + kRankMax * 4 + 64 * 8;
 
-// rank[i] = number of the n values (slot lane + 64 i holds vals[i], ids[i]) that
-// beat value i in rank_beats' order: one pass of broadcast LDS reads per wave.
-__device__ __forceinline__ void compute_ranks(const double (&vals)[4], const int (&ids)[4], int n, int lane,
-                                              void* scratch, int (&rank)[4]) {
-    uint64_t* ks = (uint64_t*)scratch;
-    int* is = (int*)(ks + kRankMax);
+// Selection of one token's top K of E <= 256 logits (lgt, in LDS) by the waves
+// first, first + step, ... of a workgroup, each taking every step-th expert. The
+// rank of expert e (how many experts beat it in rank_beats' order) is the
+// popcount of one ballot per 64 comparators, so a wave ranks an expert in a few
+// instructions with no loop over the other experts. Ranks are distinct (ties go
+// to the lower index), and the expert of rank r < K writes sel_id[r], sel_val[r]:
+// the selection in the order of repeated arg-max.
+__device__ __forceinline__ void ballot_select(const double* lgt, int E, int K, int first, int step, int lane,
+                                              int32_t* sel_id, double* sel_val) {
     uint64_t key[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        key[i] = order_key(vals[i]);
-        rank[i] = 0;
-        if (lane + 64 * i < n) {
-            ks[lane + 64 * i] = key[i];
-            is[lane + 64 * i] = ids[i];
+    for (int j = 0; j < 4; ++j) {
+        const int c = lane + 64 * j;
+        key[j] = c < E ? order_key(lgt[c]) : 0ull;
+    }
+    for (int e = first; e < E; e += step) {
+        const double v = lgt[e];
+        const uint64_t ke = order_key(v);
+        int r = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (64 * j < E) {  // wave-uniform
+                const int c = lane + 64 * j;
+                const bool beats = c < E && (key[j] > ke || (key[j] == ke && c < e));
+                r += __popcll(__ballot(beats));
+            }
+        }
+        if (lane == 0 && r < K) {
+            sel_id[r] = e;
+            sel_val[r] = v;
         }
     }
-    __builtin_amdgcn_wave_barrier();
-    for (int s2 = 0; s2 < n; ++s2) {
-        const uint64_t k2 = ks[s2];
-        const int e2 = is[s2];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) rank[i] += (k2 > key[i] || (k2 == key[i] && e2 < ids[i])) ? 1 : 0;
-    }
-    __builtin_amdgcn_wave_barrier();
 }
 
-// Top-k and softmax of n <= 256 values by one wave, select_topk's results
-// without its K dependent arg-max rounds: value i of slot lane + 64 i (id ids[i],
-// absent when the slot is >= n) gets rank = number of values that beat it, from
-// one pass over the keys in LDS; ranks 0..K-1 are the selection in order.
-__device__ __forceinline__ void rank_select(const double (&vals)[4], const int (&ids)[4], int n, int K, int lane,
-                                            void* scratch, int32_t* idx_row, float* w_row) {
-    double* sv = (double*)((char*)scratch + kRankMax * 12);  // [0, 32): selected values; [32, 64): their exps
-    int rank[4];
-    compute_ranks(vals, ids, n, lane, scratch, rank);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (lane + 64 * i < n && rank[i] < K) {
-            sv[rank[i]] = vals[i];
-            idx_row[rank[i]] = ids[i];
-        }
-    __builtin_amdgcn_wave_barrier();
-    const double m = sv[0];  // fmax over the selection = the first pick (NaN only if all are NaN)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (lane + 64 * i < n && rank[i] < K) sv[32 + rank[i]] = exp(vals[i] - m);
-    __builtin_amdgcn_wave_barrier();
+// Softmax over the K selected (ballot_select's order, whose first pick is the
+// maximum; NaN only if every logit is NaN), in fp64 with the exponentials summed
+// in selection order, rounded to fp32. One wave.
+__device__ __forceinline__ void softmax_selected(const int32_t* sel_id, const double* sel_val, int K, int lane,
+                                                 int32_t* idx_row, float* w_row) {
+    const double m = sel_val[0];
+    const double ex = lane < K ? exp(sel_val[lane < K ? lane : 0] - m) : 0.0;
     double sum = 0.0;
-    for (int j = 0; j < K; ++j) sum += sv[32 + j];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (lane + 64 * i < n && rank[i] < K) w_row[rank[i]] = (float)(sv[32 + rank[i]] / sum);
-    __builtin_amdgcn_wave_barrier();  // scratch reusable
+    for (int j = 0; j < K; ++j) sum += __shfl(ex, j, 64);
+    if (lane < K) {
+        idx_row[lane] = sel_id[lane];
+        w_row[lane] = (float)(ex / sum);
+    }
 }
 
 __device__ __forceinline__ void bf16x8_to_f32(uint4 v, float (&f)[8]) {
@@ -253,19 +247,21 @@ __global__ __launch_bounds__(kRouterThreads) void k_router(const uint16_t* __res
     }
     __syncthreads();
 
-    void* rscr = (void*)(lg + TB * E + wave * (kRankScratchBytes / 8));
-    for (int tb = wave; tb < ntb; tb += NW) {
-        const int t = t0 + tb;
-        if (E <= kRankMax) {
-            double vals[4];
-            int ids[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ids[i] = lane + 64 * i;
-                vals[i] = ids[i] < E ? lg[tb * E + ids[i]] : 0.0;
-            }
-            rank_select(vals, ids, E, K, lane, rscr, idx + (size_t)t * K, wts + (size_t)t * K);
-        } else {
+    if (E <= kRankMax) {
+        // every wave ranks a share of each token's experts, then one wave per token
+        // takes the softmax of its selection
+        double* selv = lg + TB * E;               // [TB][32]
+        int32_t* seli = (int32_t*)(selv + TB * 32);  // [TB][32]
+        for (int tb = 0; tb < ntb; ++tb)
+            ballot_select(lg + tb * E, E, K, wave, NW, lane, seli + tb * 32, selv + tb * 32);
+        __syncthreads();
+        for (int tb = wave; tb < ntb; tb += NW) {
+            const int t = t0 + tb;
+            softmax_selected(seli + tb * 32, selv + tb * 32, K, lane, idx + (size_t)t * K, wts + (size_t)t * K);
+        }
+    } else {
+        for (int tb = wave; tb < ntb; tb += NW) {
+            const int t = t0 + tb;
             select_topk(lg + tb * E, E, K, lane, idx + (size_t)t * K, wts + (size_t)t * K);
         }
     }
@@ -275,11 +271,11 @@ __global__ __launch_bounds__(kRouterThreads) void k_router(const uint16_t* __res
 // One-token route (decode at batch 1): router logits, top-k, softmax and the
 // bucketing of the k pairs in one workgroup of 16 waves, one launch instead of
 // two. Wave w computes the logits of experts w * EPI.. (every 16-byte chunk of
-// its rows loaded up front, as k_router does); wave 0 then ranks them
-// (compute_ranks, the order of rank_beats) and, since a token's k experts are
-// distinct, the stable counting sort of its k pairs by expert is the ascending
-// order of the selected ids: pair j goes to sorted position #{i : e_i < e_j}.
-// E <= 256 (the rank scratch of one wave).
+// its rows loaded up front, as k_router does); all waves then rank them
+// (ballot_select, the order of rank_beats) and wave 0 takes the softmax. Since a
+// token's k experts are distinct, the stable counting sort of its k pairs by
+// expert is the ascending order of the selected ids: pair j goes to sorted
+// position #{i : e_i < e_j}. E <= 256.
 // ---------------------------------------------------------------------------
 constexpr int kRoute1Threads = 1024;
 
@@ -289,7 +285,7 @@ __global__ __launch_bounds__(kRoute1Threads) void k_route1(
     int K, int32_t* __restrict__ idx, float* __restrict__ wts, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ pos, int4* __restrict__ slots,
     int32_t* __restrict__ n_slots, int4* __restrict__ passes, int32_t* __restrict__ n_passes, int vec) {
-    extern __shared__ double lg[];  // [E] logits | rank scratch | selected ids [32], values [32]
+    extern __shared__ double lg[];  // [E] logits | selected values [32] | selected ids [32]
     constexpr int NW = kRoute1Threads / 64;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int e0 = wave * EPI; e0 < E; e0 += NW * EPI) {
@@ -315,26 +311,11 @@ __global__ __launch_bounds__(kRoute1Threads) void k_route1(
         }
     }
     __syncthreads();
+    double* selval = lg + E;                      // [32]
+    int32_t* selid = (int32_t*)(selval + 32);     // [32]
+    ballot_select(lg, E, K, wave, NW, lane, selid, selval);
+    __syncthreads();
     if (wave != 0) return;
-
-    void* scratch = (void*)(lg + E);
-    int32_t* selid = (int32_t*)((char*)scratch + kRankScratchBytes);
-    double* selval = (double*)(selid + 32);
-    double vals[4];
-    int ids[4], rank[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        ids[i] = lane + 64 * i;
-        vals[i] = ids[i] < E ? lg[ids[i]] : 0.0;
-    }
-    compute_ranks(vals, ids, E, lane, scratch, rank);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (ids[i] < E && rank[i] < K) {
-            selid[rank[i]] = ids[i];
-            selval[rank[i]] = vals[i];
-        }
-    __builtin_amdgcn_wave_barrier();
     const int ej = lane < K ? selid[lane] : 0x7fffffff;  // pair j = lane (token 0, slot j)
     const double vj = lane < K ? selval[lane] : 0.0;
     // softmax over the k selected in selection order (the first pick is the maximum)
@@ -376,13 +357,16 @@ int route1_launch(const void* x, const void* w, const void* bias, int H, int E, 
                   void* n_passes, hipStream_t stream) {
     if (E > kRankMax || K > E || K > kMaxTopK) return set_error(PHYSLLM_MOE_EINVAL, "route1: sizes out of range");
     const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0);
-    const size_t lds = (size_t)E * sizeof(double) + kRankScratchBytes + 32 * 4 + 32 * 8;
+    const size_t lds = (size_t)E * sizeof(double) + 32 * 8 + 32 * 4;
     hipLaunchKernelGGL((k_route1<2>), dim3(1), dim3(kRoute1Threads), lds, stream, (const uint16_t*)x,
                        (const uint16_t*)w, (const uint16_t*)bias, H, E, K, (int32_t*)idx, (float*)wts,
                        (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm, (int32_t*)pos, (int4*)slots,
                        (int32_t*)n_slots, (int4*)passes, (int32_t*)n_passes, vec);
     return check_launch("route1");
 }
+
+// logits [TB][E] (fp64), then the selections [TB][32] (fp64 values, int ids)
+static size_t router_smem_bytes(int TB, int E) { return (size_t)TB * E * sizeof(double) + (size_t)TB * 32 * 12; }
 
 int router_launch(const void* x, const void* w, const void* bias, int B, int H, int E, int K, void* idx,
                   void* wts, hipStream_t stream) {
@@ -396,12 +380,12 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
         // prefill: 4 tokens per group share every loaded router row
         constexpr int TB = 4;
         hipLaunchKernelGGL((k_router<TB, 1, 4>), dim3((B + TB - 1) / TB), dim3(kRouterThreads),
-                           (size_t)TB * E * sizeof(double) + (kRouterThreads / 64) * kRankScratchBytes, stream, (const uint16_t*)x, (const uint16_t*)w,
+                           router_smem_bytes(TB, E), stream, (const uint16_t*)x, (const uint16_t*)w,
                            (const uint16_t*)bias, B, H, E, K, (int32_t*)idx, (float*)wts, vec);
     } else {
         // decode: one token per group, 4 experts' rows in flight per wave
         hipLaunchKernelGGL((k_router<1, 4, 6>), dim3(B), dim3(kRouterThreads),
-                           (size_t)E * sizeof(double) + (kRouterThreads / 64) * kRankScratchBytes, stream,
+                           router_smem_bytes(1, E), stream,
                            (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, B, H, E, K,
                            (int32_t*)idx, (float*)wts, vec);
     }

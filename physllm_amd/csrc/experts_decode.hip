@@ -32,6 +32,8 @@ namespace physllm {
 constexpr int kGemvThreads = 256;  // 4 waves, each one 16-row weight tile at a time
 constexpr int kGemvNit = 23;       // k-steps of 4 MX blocks held in registers: 92 blocks = 2944 elements
 constexpr int kPassTok = 8;        // tokens staged in LDS per pass
+constexpr int kGemvSclSlice = 128 * 16;  // bytes of a wave's scale slice: 16 x NB <= 1472, then unread padding
+constexpr uint32_t kRsrcPast = 0xfffff000u;  // a buffer offset past any expert's range (a load there reads zeros)
 constexpr int kStageU = 4;         // 16-byte activation loads in flight per thread while staging
 constexpr int kMaxScaleBlocks = 256;  // K <= 8192: a tile's scales (16 x NB bytes) fit a wave's LDS slice
 
@@ -214,17 +216,20 @@ __device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t
 
 // Fast form for K ranges of at most 92 MX blocks (2944 elements: GPT-OSS H = I =
 // 2880 = 90 blocks), one 16-row tile per wave, loads in this order:
-//   1. the expert slot (scalar load), then the wave's 23 weight stripes (16
-//      bytes per lane each: 16 rows x 64 contiguous bytes per wave) and the
-//      tile's scales (two 16-byte loads per lane) — the bulk of the bytes is in
-//      flight after a single dependent load;
-//   2. the first pass's token rows (scalar loads of the sorted pair ids) and the
-//      activation units this thread stages (NS 16-byte loads).
-// Everything is then stored to LDS once, one barrier, and the 23 k-steps run
-// from registers and LDS. Experts with more than 8 tokens
-// run further passes against the same registers.
+//   1. the expert slot and the first pass's token rows (scalar loads of the
+//      sorted pair ids; none at batch 1, where every pair reads row 0);
+//   2. the activation units this thread stages (NS 16-byte loads) and the tile's
+//      scales (two 16-byte loads per lane);
+//   3. the wave's 23 weight stripes (16 bytes per lane each: 16 rows x 64
+//      contiguous bytes per wave).
+// Vector loads retire in issue order, so staging the small loads to LDS (one
+// barrier) waits only for them, and the 23 k-steps then run as the stripes
+// arrive instead of after the last one. The pair ids come in as a restrict
+// kernel argument, so they are read with scalar loads, which do not wait behind
+// the vector loads. Experts with more than 8 tokens run further passes against
+// the same registers.
 template <int MODE, int NS>
-__global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p) {
+__global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p, const int32_t* __restrict__ perm) {
     extern __shared__ uint4 lds[];
     const int4 si = p.slots[blockIdx.y];  // {expert, tokens, first sorted position, 0}
     const int e = si.x, ne = si.y, p0 = si.z;
@@ -243,22 +248,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p) {
     const uint32_t exp_w = (uint32_t)p.R * row_bytes;   // one expert's codes
     const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;  // one expert's scales
 
-    uint8_t* scl = (uint8_t*)lds + wave * 16 * 96;  // this wave's tile scales [16][NB <= 92]
-    uint4* xs = lds + (4 * 16 * 96) / 16;          // activations [kPassTok][su]
+    uint8_t* scl = (uint8_t*)lds + wave * kGemvSclSlice;  // this wave's tile scales [16][NB <= 92]
+    uint4* xs = lds + (kGemvThreads / 64) * kGemvSclSlice / 16;  // activations [kPassTok][su]
 
-    // ---- 1. weights and scales (rows past R read zeros) ----
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.blocks + (size_t)e * exp_w, exp_w);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales + (size_t)e * exp_s, exp_s);
-    const uint32_t woff = (uint32_t)(r0 + m) * row_bytes + (uint32_t)(kb0 + g) * 16u;
-    u32x4_t wq[kGemvNit];
-#pragma unroll
-    for (int j = 0; j < kGemvNit; ++j)  // only the k-steps of this split's K range
-        wq[j] = (4 * j < nblk) ? buf_load16(rw, woff, 64 * j) : u32x4_t{0u, 0u, 0u, 0u};
-    const uint32_t soff = (uint32_t)r0 * NB + lane * 16u;  // 16 rows x NB bytes, contiguous
-    const u32x4_t sv0 = buf_load16(rs, soff, 0);
-    const u32x4_t sv1 = buf_load16(rs, soff, 1024);
-
-    // ---- 2. activations of pass 0 ----
     const __amdgpu_buffer_rsrc_t ract = make_rsrc(p.act, (uint32_t)p.act_rows * (uint32_t)p.Kdim * 2u);
     auto stage_load = [&](int tb, u32x4_t (&v)[NS]) {
         // lane r < kPassTok holds the activation row of pass row r (scalar loads of
@@ -267,7 +259,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p) {
 #pragma unroll
         for (int r = 0; r < kPassTok; ++r) {
             const int q = min(tb + r, ne - 1);
-            const int id = (MODE == kModeGateUp) ? p.perm[p0 + q] / p.top_k : p0 + q;
+            const int id = (MODE == kModeGateUp) ? (p.act_rows == 1 ? 0 : perm[p0 + q] / p.top_k) : p0 + q;
             rowid = (lane == r) ? id : rowid;
         }
 #pragma unroll
@@ -291,26 +283,35 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p) {
         }
     };
     int ntok = min(kPassTok, ne);
+    u32x4_t wq[kGemvNit];
     {
+        // ---- activations of pass 0 and the tile's scales, then the weights (rows past R read zeros)
         u32x4_t xv[NS];
         stage_load(0, xv);
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales + (size_t)e * exp_s, exp_s);
+        const uint32_t soff = (uint32_t)r0 * NB + lane * 16u;  // 16 rows x NB bytes, contiguous
+        const u32x4_t sv0 = buf_load16(rs, soff, 0);
+        const u32x4_t sv1 = buf_load16(rs, soff, 1024);
         __builtin_amdgcn_sched_barrier(0);
-        if (lane < NB) ((u32x4_t*)scl)[lane] = sv0;
-        if (lane + 64 < NB) ((u32x4_t*)scl)[lane + 64] = sv1;
+        const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.blocks + (size_t)e * exp_w, exp_w);
+        const uint32_t woff = (uint32_t)(r0 + m) * row_bytes + (uint32_t)(kb0 + g) * 16u;
+        // k-steps past this split's K range load from past the buffer's end (zeros,
+        // no memory traffic): straight-line loads, no branch for a load to sink into
+#pragma unroll
+        for (int j = 0; j < kGemvNit; ++j) wq[j] = buf_load16(rw, 4 * j < nblk ? woff : kRsrcPast, 64 * j);
+        __builtin_amdgcn_sched_barrier(0);
+        // every lane stores both scale units (the slice holds 128; units past the
+        // tile's 16 x NB bytes are never read): a store under `lane < NB` would let
+        // the compiler sink its load into the branch, behind the weight stripes
+        ((u32x4_t*)scl)[lane] = sv0;
+        ((u32x4_t*)scl)[lane + 64] = sv1;
         stage_store(ntok, xv);
     }
     __syncthreads();
 
     const bool row_ok = r0 < p.R;
-    for (int tb = 0; tb < ne; tb += kPassTok) {
-        if (tb > 0) {
-            ntok = min(kPassTok, ne - tb);
-            u32x4_t xn[NS];
-            stage_load(tb, xn);
-            __syncthreads();  // every wave finished reading the previous pass
-            stage_store(ntok, xn);
-            __syncthreads();
-        }
+    // one pass: the 23 k-steps against the staged tokens tb..tb+ntok-1, then the epilogue
+    auto run_pass = [&](int tb) {
         // lane's column of the B fragment at block 4j+g; lanes past the pass's tokens
         // read a valid row (an MFMA output column depends only on its own B column,
         // and those columns are not stored)
@@ -340,7 +341,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p) {
             }
         }
         const bool tv = m < ntok;
-        if (!row_ok || !tv) continue;
+        if (!row_ok || !tv) return;
         const f32x4_t acc = (acc0 + acc1) + (acc2 + acc3);
         const int pp = p0 + tb + m;  // sorted position of this lane's token
         const int rr = r0 + 4 * g;
@@ -367,6 +368,18 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p) {
             float* ybase = (float*)p.out + (size_t)split * p.n_pairs * p.R;
             *(float4*)(ybase + (size_t)pp * p.R + rr) = y;
         }
+    };
+    // the first pass outside the loop: its k-steps wait for each stripe as it
+    // arrives (inside a loop the first use of the stripes waits for all of them)
+    run_pass(0);
+    for (int tb = kPassTok; tb < ne; tb += kPassTok) {
+        ntok = min(kPassTok, ne - tb);
+        u32x4_t xn[NS];
+        stage_load(tb, xn);
+        __syncthreads();  // every wave finished reading the previous pass
+        stage_store(ntok, xn);
+        __syncthreads();
+        run_pass(tb);
     }
 }
 
@@ -390,7 +403,10 @@ constexpr int kStreamThreads = 64 * kStreamWaves;
 constexpr int kSetRows = 16 * kStreamWaves;
 constexpr int kStreamRowLoads = 6;  // 64-unit loads per staged row: K ranges of <= 384 units (96 blocks)
 constexpr int kStreamRowStride = 64 * kStreamRowLoads + 1;  // LDS row stride of the staged activations
-constexpr int kStreamMaxNB = 96;    // a tile's scales (16 x NB bytes) fit a wave's 1536-byte slice
+// bytes of one wave's scale slice in the streaming kernel: the 128 16-byte units
+// its lanes store (the tile's 16 x NB <= 1536 bytes, then unread padding)
+constexpr int kStreamSclSlice = 128 * 16;
+constexpr int kStreamMaxNB = 96;    // a tile's scales (16 x NB bytes) fit in the first 1536 bytes of the slice
 
 struct StreamItem {
     int e, ne, p0, kb0, nblk, split, r0, key;  // key: pass entry and split (same key = same activations)
@@ -489,8 +505,8 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
     const uint32_t exp_b = p.bias ? (uint32_t)p.R * 2u : 0u;  // empty range: the bias reads as zero
     const uint32_t act_bytes = (uint32_t)p.act_rows * (uint32_t)p.Kdim * 2u;
     uint4* xs = lds;                                                     // [16][su]
-    uint8_t* scl0 = (uint8_t*)(lds + kPassRows * su) + wave * 16 * 96;  // [2 bufs][8 waves][16][NB <= 96]
-    constexpr int kSclBuf = kStreamWaves * 16 * 96;
+    uint8_t* scl0 = (uint8_t*)(lds + kPassRows * su) + wave * kStreamSclSlice;  // [2 bufs][8 waves][slice]
+    constexpr int kSclBuf = kStreamWaves * kStreamSclSlice;
 
     // loads of one item's side data: 16 rows of scales, this lane's 4 biases and
     // (when `act` is set) the item's activation rows 2w, 2w+1 — as 64-unit
@@ -515,10 +531,14 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
             for (int u = 0; u < kStreamRowLoads; ++u) av[r2][u] = buf_load16(ra, voff, 1024 * u);
         }
     };
-    auto scale_store = [&](int b) {  // wave-private slice: no barrier
+    // wave-private slice: no barrier. Every lane stores both units (the slice holds
+    // 128; units past the tile's 16 x NB bytes are never read): a store under
+    // `lane < NB` lets the compiler sink the scale load into that branch, behind
+    // the item's weight stripes, and wait for all of them.
+    auto scale_store = [&](int b) {
         uint8_t* s = scl0 + b * kSclBuf;
-        if (lane < NB) ((u32x4_t*)s)[lane] = sv0;
-        if (lane + 64 < NB) ((u32x4_t*)s)[lane + 64] = sv1;
+        ((u32x4_t*)s)[lane] = sv0;
+        ((u32x4_t*)s)[lane + 64] = sv1;
     };
     // unconditional stores: rows past the item's tokens repeat its last row and units
     // past its K range hold the next row's elements, and neither is ever read
@@ -539,8 +559,12 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
         return (uint32_t)(it.r0 + m) * row_bytes + (uint32_t)(it.kb0 + g) * 16u;
     };
 
-    // prologue: the first item's weights, then its side data
+    // prologue: the first item's side data, then its weights — the order of the
+    // steady state (an item's side data is issued before its stripes), so the
+    // staging below waits only for the small loads and the k-loop (which issues
+    // the next item's loads) starts while the stripes stream in
     StreamItem cur = stream_item(p, passes, f0, sets, per, NB, wave);
+    side_load(cur, true);
     u32x4_t wq[kGemvNit];
     {
         const __amdgpu_buffer_rsrc_t rw = wrsrc(cur, true);
@@ -548,7 +572,6 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
 #pragma unroll
         for (int j = 0; j < kGemvNit; ++j) wq[j] = buf_load16(rw, voff, 64 * j);
     }
-    side_load(cur, true);
     uint2 bcur = bnx;
     scale_store(0);
     act_store();
@@ -662,7 +685,7 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
         // many touched experts: persistent streaming kernel, one 8-wave group per CU
         // (a multiple of 8 groups: the item order is XCD-aware)
         const unsigned grid = (unsigned)((n_cu + 7) & ~7);
-        const size_t lds = (size_t)kPassRows * kStreamRowStride * 16 + (size_t)2 * kStreamWaves * 16 * 96;
+        const size_t lds = (size_t)kPassRows * kStreamRowStride * 16 + (size_t)2 * kStreamWaves * kStreamSclSlice;
         p.rt = 1;
         if (mode == kModeGateUp)
             hipLaunchKernelGGL(k_mx_gemv_stream<kModeGateUp>, dim3(grid), dim3(kStreamThreads), lds, stream, p,
@@ -674,15 +697,15 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
         // activation units one thread stages per pass: ntok rows x 4*per 16-byte units
         const int units = ntok * 4 * per;
         const int ns = (units + kGemvThreads - 1) / kGemvThreads;
-        const size_t lds = (size_t)4 * 16 * 96 + (size_t)kPassTok * (4 * per + 1) * 16;
+        const size_t lds = (size_t)(kGemvThreads / 64) * kGemvSclSlice + (size_t)kPassTok * (4 * per + 1) * 16;
         dim3 grid(sets, max_slots, p.split);
         p.rt = 1;
         if (ns <= 2) {
-            if (mode == kModeGateUp) hipLaunchKernelGGL((k_mx_gemv<kModeGateUp, 2>), grid, dim3(kGemvThreads), lds, stream, p);
-            else hipLaunchKernelGGL((k_mx_gemv<kModeDown, 2>), grid, dim3(kGemvThreads), lds, stream, p);
+            if (mode == kModeGateUp) hipLaunchKernelGGL((k_mx_gemv<kModeGateUp, 2>), grid, dim3(kGemvThreads), lds, stream, p, p.perm);
+            else hipLaunchKernelGGL((k_mx_gemv<kModeDown, 2>), grid, dim3(kGemvThreads), lds, stream, p, p.perm);
         } else {
-            if (mode == kModeGateUp) hipLaunchKernelGGL((k_mx_gemv<kModeGateUp, 12>), grid, dim3(kGemvThreads), lds, stream, p);
-            else hipLaunchKernelGGL((k_mx_gemv<kModeDown, 12>), grid, dim3(kGemvThreads), lds, stream, p);
+            if (mode == kModeGateUp) hipLaunchKernelGGL((k_mx_gemv<kModeGateUp, 12>), grid, dim3(kGemvThreads), lds, stream, p, p.perm);
+            else hipLaunchKernelGGL((k_mx_gemv<kModeDown, 12>), grid, dim3(kGemvThreads), lds, stream, p, p.perm);
         }
     } else {
         const int seg = 4 * kGemvNit;

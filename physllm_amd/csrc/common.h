@@ -70,6 +70,19 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t 
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// ---- buffer loads -----------------------------------------------------------
+// A raw buffer over [base, base + bytes): loads past the range read zeros and
+// make no memory access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+
+constexpr uint32_t kRsrcPast = 0xfffff000u;  // an offset past any buffer range used here (a load there reads zeros)
+
+__device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, int imm) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff + (uint32_t)imm, 0, 0);
+}
+
 // ---- activation -------------------------------------------------------------
 // Clamped SwiGLU of GPT-OSS: g = min(g, limit), u = clamp(u, -limit, limit),
 // g * sigmoid(alpha g) * (u + 1); comparisons keep NaN.

@@ -33,7 +33,6 @@ constexpr int kGemvThreads = 256;  // 4 waves, each one 16-row weight tile at a 
 constexpr int kGemvNit = 23;       // k-steps of 4 MX blocks held in registers: 92 blocks = 2944 elements
 constexpr int kPassTok = 8;        // tokens staged in LDS per pass
 constexpr int kGemvSclSlice = 128 * 16;  // bytes of a wave's scale slice: 16 x NB <= 1472, then unread padding
-constexpr uint32_t kRsrcPast = 0xfffff000u;  // a buffer offset past any expert's range (a load there reads zeros)
 constexpr int kStageU = 4;         // 16-byte activation loads in flight per thread while staging
 constexpr int kMaxScaleBlocks = 256;  // K <= 8192: a tile's scales (16 x NB bytes) fit a wave's LDS slice
 
@@ -206,14 +205,6 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv_generic(GemvParams p) 
 // range-checked memory from `base`; loads past the range return zeros, so tile
 // edges need no clamped (per-load) addresses and the k-step of a load is an
 // immediate offset.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, int imm) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, voff + (uint32_t)imm, 0, 0);
-}
-
 // Fast form for K ranges of at most 92 MX blocks (2944 elements: GPT-OSS H = I =
 // 2880 = 90 blocks), one 16-row tile per wave, loads in this order:
 //   1. the expert slot and the first pass's token rows (scalar loads of the

@@ -365,6 +365,299 @@ int route1_launch(const void* x, const void* w, const void* bias, int H, int E, 
     return check_launch("route1");
 }
 
+// ---------------------------------------------------------------------------
+// Two-pass router for batches of kRmxMinBatch tokens or more (E <= 128,
+// H % 32 == 0, H <= kRmxMaxH): one workgroup of 8 waves per 16 tokens, the
+// tokens' rows staged once in LDS.
+//  1. Approximate logits on the matrix cores (bf16 MFMA, fp32 accumulation):
+//     a[t][e] = sum x*w, with S = sum |x||w|, W1[e] = sum |w| and X1[t] = sum |x|
+//     from three more MFMAs on sign-cleared operands and ones. Each 32-term MFMA
+//     adds at most 33 roundings to a chain of H/32 of them, so
+//     |a + b - exact| <= eps = g/(1-g) (S + c) + c + 2^-126 (W1 + X1)(1 + 2g) + u|a + b|
+//     with u = 2^-23 (covers truncating as well as rounding adders), g = m u / (1 - m u)
+//     for m = 33 H/32 + 16 roundings, c bounding products and partial sums the
+//     hardware may flush below 2^-126, and the W1/X1 term the products of an
+//     input it may flush as subnormal.
+//  2. Candidates: expert e can be among the k largest exact logits only if
+//     a + b + eps >= T, the k-th largest a + b - eps (k experts have exact logits
+//     >= T). A token with any non-finite approximate sum (overflow, inf, NaN) makes
+//     all its experts candidates.
+//  3. Exact logits of the candidates only, as k_router computes them (fp32
+//     products, fp64 sums in the same lane order and wave reduction, + bias), then
+//     the selection (ballot_select) and softmax among the candidates: the same
+//     indices and weights as ranking every exact logit.
+// ---------------------------------------------------------------------------
+constexpr int kRmxTok = 16;
+constexpr int kRmxThreads = 512;
+constexpr int kRmxWaves = kRmxThreads / 64;
+constexpr int kRmxMaxE = 128;  // experts per token the LDS layout holds (taken above 64 only for large batches:
+                               // a workgroup streams all E rows, and few workgroups stream slowly)
+constexpr int kRmxMaxH = 3072;  // the LDS layout of k_router_mx fits 160 KiB up to here
+constexpr int kRmxMinBatch = 128;
+
+// LDS layout of k_router_mx (bytes): token rows | partial sums | W1/X1 partials |
+// bounds | candidate ids | candidate counts + flags | exact logits | selections
+struct RmxLayout {
+    uint32_t xstride, red, wx, lohi, cand, cnt, exact, sel, total;
+};
+
+__host__ __device__ inline RmxLayout rmx_layout(int H) {
+    RmxLayout L;
+    L.xstride = (uint32_t)H * 2u + 16u;                    // odd multiple of 16 bytes per row
+    L.red = kRmxTok * L.xstride;                           // [8 waves][8][64] f32: a (4), S (4)
+    L.wx = L.red + kRmxWaves * 8 * 64 * 4;                 // [8 waves][32] f32: W1 (16), X1 (16)
+    L.lohi = L.wx + kRmxWaves * 32 * 4;                    // [16][kRmxMaxE][2] f32: lower, upper bound
+    L.cand = L.lohi + kRmxTok * kRmxMaxE * 8;              // [16][kRmxMaxE] i32 candidate expert ids
+    L.cnt = L.cand + kRmxTok * kRmxMaxE * 4;               // [16] counts, [16] all-candidate flags
+    L.exact = L.cnt + 2 * kRmxTok * 4;                     // [16][kRmxMaxE] f64 exact logits
+    L.sel = L.exact + kRmxTok * kRmxMaxE * 8;              // [16][32] f64 values, [16][32] i32 ids
+    L.total = L.sel + kRmxTok * 32 * 12;
+    return L;
+}
+
+// |v| of 8 packed bf16 (sign bits cleared)
+__device__ __forceinline__ uint4 bf16x8_abs(uint4 v) {
+    return make_uint4(v.x & 0x7fff7fffu, v.y & 0x7fff7fffu, v.z & 0x7fff7fffu, v.w & 0x7fff7fffu);
+}
+
+__global__ __launch_bounds__(kRmxThreads) void k_router_mx(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ bias, int B, int H,
+                                                           int E, int K, int32_t* __restrict__ idx,
+                                                           float* __restrict__ wts) {
+    extern __shared__ uint4 lds4[];
+    char* lds = (char*)lds4;
+    const RmxLayout L = rmx_layout(H);
+    const int t0 = blockIdx.x * kRmxTok;
+    const int ntok = min(kRmxTok, B - t0);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int m = lane & 15, g = lane >> 4;
+    const int nc = H >> 5;   // 32-element chunks
+    const int nch = H >> 3;  // 8-element chunks (exact pass)
+
+    // ---- stage the tokens' rows (rows past B are zero): every load of a thread is
+    // issued before its first store, so the rows arrive in one memory round trip ----
+    {
+        const uint32_t units = (uint32_t)nch;  // 16-byte units per row
+        const uint32_t total = kRmxTok * units;
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)t0 * H, (uint32_t)ntok * (uint32_t)H * 2u);
+        constexpr int SU = (kRmxTok * (kRmxMaxH / 8) + kRmxThreads - 1) / kRmxThreads;  // 12 units per thread at most
+        u32x4_t v[SU];
+#pragma unroll
+        for (int k2 = 0; k2 < SU; ++k2) {
+            const uint32_t i = tid + k2 * kRmxThreads;  // unit i = row * units + column; past the tile: no load
+            const uint32_t r = i / units, c = i - r * units;
+            v[k2] = buf_load16(rx, i < total ? (r * (uint32_t)H + c * 8u) * 2u : kRsrcPast, 0);
+        }
+#pragma unroll
+        for (int k2 = 0; k2 < SU; ++k2) {
+            const uint32_t i = tid + k2 * kRmxThreads;
+            const uint32_t r = i / units, c = i - r * units;
+            if (i < total) *(u32x4_t*)(lds + r * L.xstride + c * 16u) = v[k2];
+        }
+    }
+    int* cnt = (int*)(lds + L.cnt);
+    if (tid < 2 * kRmxTok) cnt[tid] = 0;
+    __syncthreads();
+
+    // ---- 1. approximate sums: wave = (expert tile, K part) ----
+    const int nt = (E + 15) >> 4;
+    const int nt8 = nt <= 1 ? 1 : nt <= 2 ? 2 : nt <= 4 ? 4 : 8;
+    const int nk = kRmxWaves / nt8;
+    const int tile = wave % nt8, kp = wave / nt8;
+    const int cb = kp * nc / nk, ce = (kp + 1) * nc / nk;
+    {
+        const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)E * (uint32_t)H * 2u);
+        const uint32_t wrow = (uint32_t)(tile * 16 + m) * (uint32_t)H * 2u + (uint32_t)g * 16u;
+        const char* xrow = lds + m * L.xstride + g * 16;
+        const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, accS = acc, accW = acc, accX = acc;
+        constexpr int D = 8;  // weight chunks in flight per wave
+        u32x4_t wb[D];
+#pragma unroll
+        for (int i = 0; i < D; ++i) wb[i] = buf_load16(rw, cb + i < ce ? wrow + (uint32_t)(cb + i) * 64u : kRsrcPast, 0);
+        for (int c0 = cb; c0 < ce; c0 += D) {
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                const int c = c0 + i;
+                if (c < ce) {  // wave-uniform
+                    const uint4 xv = *(const uint4*)(xrow + c * 64);
+                    const u32x4_t q = wb[i];
+                    const uint4 wv = make_uint4(q[0], q[1], q[2], q[3]);
+                    const uint4 wa = bf16x8_abs(wv), xa = bf16x8_abs(xv);
+                    acc = mfma16x16x32(as_bf16x8(wv), as_bf16x8(xv), acc);
+                    accS = mfma16x16x32(as_bf16x8(wa), as_bf16x8(xa), accS);
+                    accW = mfma16x16x32(as_bf16x8(wa), as_bf16x8(ones), accW);
+                    accX = mfma16x16x32(as_bf16x8(ones), as_bf16x8(xa), accX);
+                }
+                wb[i] = buf_load16(rw, c + D < ce ? wrow + (uint32_t)(c + D) * 64u : kRsrcPast, 0);
+            }
+        }
+        // partials: lane holds rows (experts) 4g + i of the tile, column (token) m
+        float* red = (float*)(lds + L.red) + wave * 8 * 64;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            red[i * 64 + lane] = acc[i];
+            red[(4 + i) * 64 + lane] = accS[i];
+        }
+        float* wx = (float*)(lds + L.wx) + wave * 32;
+        if (m == 0)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wx[4 * g + i] = accW[i];  // sum |w| of row 4g + i
+        if (g == 0) wx[16 + m] = accX[0];                         // sum |x| of token m
+    }
+    __syncthreads();
+
+    // ---- bounds: the waves of K part 0 sum the parts in order ----
+    const float u = 0x1p-23f;
+    if (kp == 0) {
+        const double mr = 33.0 * nc + 16.0;
+        const double gm = mr * (double)u / (1.0 - mr * (double)u);
+        const double cab = (33.0 * nc + H + 16.0) * 0x1p-125;
+        float a[4] = {0.f, 0.f, 0.f, 0.f}, S[4] = {0.f, 0.f, 0.f, 0.f}, W1[4] = {0.f, 0.f, 0.f, 0.f}, X1 = 0.f;
+        for (int p2 = 0; p2 < nk; ++p2) {
+            const int w2 = p2 * nt8 + tile;
+            const float* red = (const float*)(lds + L.red) + w2 * 8 * 64;
+            const float* wx = (const float*)(lds + L.wx) + w2 * 32;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[i] += red[i * 64 + lane];
+                S[i] += red[(4 + i) * 64 + lane];
+                W1[i] += wx[4 * g + i];
+            }
+            X1 += wx[16 + m];
+        }
+        float2* lohi = (float2*)(lds + L.lohi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = tile * 16 + 4 * g + i;
+            if (e < E && m < ntok) {
+                const float bb = bias ? bf16_to_f32(bias[e]) : 0.f;
+                const float ab = a[i] + bb;
+                const double eps = gm / (1.0 - gm) * ((double)S[i] + cab) + cab +
+                                   0x1p-126 * ((double)W1[i] + (double)X1) * (1.0 + 2.0 * gm) +
+                                   (double)u * fabs((double)ab);
+                const bool fin = __builtin_isfinite(ab) && __builtin_isfinite(S[i]) && __builtin_isfinite(W1[i]) &&
+                                 __builtin_isfinite(X1) && __builtin_isfinite(eps);
+                if (!fin) atomicOr(&cnt[kRmxTok + m], 1);
+                const double e2 = eps * (1.0 + 0x1p-20);
+                lohi[m * kRmxMaxE + e] = make_float2(__double2float_rd((double)ab - e2), __double2float_ru((double)ab + e2));
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 2. candidates of token t: wave t % 8 ----
+    int32_t* cand = (int32_t*)(lds + L.cand);
+    for (int t = wave; t < ntok; t += kRmxWaves) {
+        const float2* lh = (const float2*)(lds + L.lohi) + t * kRmxMaxE;
+        const bool all = cnt[kRmxTok + t] != 0;
+        const bool v0 = lane < E, v1 = lane + 64 < E;
+        const float2 q0 = v0 ? lh[lane] : make_float2(0.f, 0.f);
+        const float2 q1 = v1 ? lh[lane + 64] : make_float2(0.f, 0.f);
+        bool c0 = v0, c1 = v1;
+        if (!all) {
+            // T = k-th largest lower bound: k rounds, each removing one largest
+            float l0 = v0 ? q0.x : -INFINITY, l1 = v1 ? q1.x : -INFINITY;
+            bool r0 = !v0, r1 = !v1;  // removed
+            float T = -INFINITY;
+            for (int j = 0; j < K; ++j) {
+                float mx = fmaxf(r0 ? -INFINITY : l0, r1 ? -INFINITY : l1);
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+                T = mx;
+                // remove one element equal to the maximum (the lowest slot)
+                const uint64_t b0 = __ballot(!r0 && l0 == mx), b1 = __ballot(!r1 && l1 == mx);
+                if (b0) {
+                    if (lane == __builtin_ctzll(b0)) r0 = true;
+                } else if (b1) {
+                    if (lane == __builtin_ctzll(b1)) r1 = true;
+                }
+            }
+            c0 = v0 && q0.y >= T;
+            c1 = v1 && q1.y >= T;
+        }
+        const uint64_t m0 = __ballot(c0), m1 = __ballot(c1);
+        const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        const int n0 = __popcll(m0);
+        if (c0) cand[t * kRmxMaxE + __popcll(m0 & lt)] = lane;
+        if (c1) cand[t * kRmxMaxE + n0 + __popcll(m1 & lt)] = lane + 64;
+        if (lane == 0) cnt[t] = n0 + __popcll(m1);
+    }
+    __syncthreads();
+
+    // ---- 3. exact logits of the candidates: pairs (t, j) over all waves, two at a time ----
+    int poff[kRmxTok + 1];
+    poff[0] = 0;
+#pragma unroll
+    for (int t = 0; t < kRmxTok; ++t) poff[t + 1] = poff[t] + (t < ntok ? cnt[t] : 0);
+    const int npairs = poff[kRmxTok];
+    double* exact = (double*)(lds + L.exact);
+    auto pair_at = [&](int p, int& t, int& j) {
+        t = 0;
+#pragma unroll
+        for (int i = 1; i < kRmxTok; ++i) t += (p >= poff[i]) ? 1 : 0;
+        j = p - poff[t];
+    };
+    const int nu = (nch + 63) >> 6;  // 8-element chunks per lane
+    for (int p = wave * 2; p < npairs; p += kRmxWaves * 2) {
+        int ta, ja, tb2, jb;
+        pair_at(p, ta, ja);
+        const bool hb = p + 1 < npairs;
+        pair_at(hb ? p + 1 : p, tb2, jb);
+        const int ea = cand[ta * kRmxMaxE + ja], eb = cand[tb2 * kRmxMaxE + jb];
+        const uint4* wa = (const uint4*)(w + (size_t)ea * H);
+        const uint4* wbp = (const uint4*)(w + (size_t)eb * H);
+        const char* xa = lds + ta * L.xstride;
+        const char* xb = lds + tb2 * L.xstride;
+        double sa = 0.0, sb = 0.0;
+        for (int u0 = 0; u0 < nu; u0 += 6) {
+            uint4 qa[6], qb[6];
+#pragma unroll
+            for (int i = 0; i < 6; ++i) {
+                const int c = lane + 64 * (u0 + i);
+                qa[i] = c < nch ? wa[c] : make_uint4(0, 0, 0, 0);
+                qb[i] = c < nch ? wbp[c] : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 6; ++i) {
+                const int c = lane + 64 * (u0 + i);
+                if (u0 + i < nu) {
+                    const uint4 va = c < nch ? *(const uint4*)(xa + c * 16) : make_uint4(0, 0, 0, 0);
+                    const uint4 vb = c < nch ? *(const uint4*)(xb + c * 16) : make_uint4(0, 0, 0, 0);
+                    float xf[8], wf[8];
+                    bf16x8_to_f32(va, xf);
+                    bf16x8_to_f32(qa[i], wf);
+#pragma unroll
+                    for (int k2 = 0; k2 < 8; ++k2) sa = acc_prod(sa, xf[k2], wf[k2]);
+                    bf16x8_to_f32(vb, xf);
+                    bf16x8_to_f32(qb[i], wf);
+#pragma unroll
+                    for (int k2 = 0; k2 < 8; ++k2) sb = acc_prod(sb, xf[k2], wf[k2]);
+                }
+            }
+        }
+        const double ra = wave_sum_f64(sa), rb = wave_sum_f64(sb);
+        if (lane == 0) {
+            exact[ta * kRmxMaxE + ja] = ra + (bias ? (double)bf16_to_f32(bias[ea]) : 0.0);
+            if (hb) exact[tb2 * kRmxMaxE + jb] = rb + (bias ? (double)bf16_to_f32(bias[eb]) : 0.0);
+        }
+    }
+    __syncthreads();
+
+    // ---- selection among the candidates, in candidate (= expert id) order ----
+    double* selv = (double*)(lds + L.sel);
+    int32_t* seli = (int32_t*)(selv + kRmxTok * 32);
+    for (int t = wave; t < ntok; t += kRmxWaves) {
+        ballot_select(exact + t * kRmxMaxE, cnt[t], K, 0, 1, lane, seli + t * 32, selv + t * 32);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < K) seli[t * 32 + lane] = cand[t * kRmxMaxE + seli[t * 32 + lane]];
+        __builtin_amdgcn_wave_barrier();
+        softmax_selected(seli + t * 32, selv + t * 32, K, lane, idx + (size_t)(t0 + t) * K,
+                         wts + (size_t)(t0 + t) * K);
+    }
+}
+
 // logits [TB][E] (fp64), then the selections [TB][32] (fp64 values, int ids)
 static size_t router_smem_bytes(int TB, int E) { return (size_t)TB * E * sizeof(double) + (size_t)TB * 32 * 12; }
 
@@ -376,7 +669,20 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
     if (B == 0) return ok();
     if (!x || !w || !idx || !wts) return set_error(PHYSLLM_MOE_EINVAL, "router: null pointer");
     const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0);
-    if (B > 1024) {
+    if (B >= kRmxMinBatch && E <= kRmxMaxE && H % 32 == 0 && H <= kRmxMaxH && vec &&
+        (E <= 64 || (int64_t)B * E >= 64 * 4096)) {
+        // two passes: matrix-core bounds, exact fp64 logits of the candidates only
+        const RmxLayout Lr = rmx_layout(H);
+        static bool attr_set = false;
+        if (!attr_set) {
+            (void)hipFuncSetAttribute((const void*)k_router_mx, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)rmx_layout(kRmxMaxH).total);
+            attr_set = true;
+        }
+        hipLaunchKernelGGL(k_router_mx, dim3((B + kRmxTok - 1) / kRmxTok), dim3(kRmxThreads), (size_t)Lr.total, stream,
+                           (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, B, H, E, K, (int32_t*)idx,
+                           (float*)wts);
+    } else if (B > 1024) {
         // prefill: 4 tokens per group share every loaded router row
         constexpr int TB = 4;
         hipLaunchKernelGGL((k_router<TB, 1, 4>), dim3((B + TB - 1) / TB), dim3(kRouterThreads),

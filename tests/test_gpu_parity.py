@@ -153,12 +153,15 @@ def _router_case(oracle, x, w, b, K):
     return host(idx)
 
 
-def test_router_near_ties_decided_in_fp64(oracle):
+@pytest.mark.parametrize("B", [48, 160])
+def test_router_near_ties_decided_in_fp64(oracle, B):
     """Experts whose logits differ by one bf16 ulp of one weight (far below the
-    fp32 matrix-core error bound): the order comes from the fp64 recomputation.
-    Experts 3 and 7 lead every token; 10, 11 and 12 compete for the 4th pick."""
+    fp32 matrix-core error bound of the two-pass router, which B = 160 takes):
+    the order comes from the exact fp64 logits. Experts 3 and 7 lead every token;
+    10, 11 and 12 compete for the 4th pick."""
+    say(f"router near ties B={B}")
     rng = np.random.default_rng(5)
-    B, H, E, K = 48, 2880, 32, 4
+    H, E, K = 2880, 32, 4
     xf = rng.standard_normal((B, H), dtype=np.float32)
     xf[:, 100] = np.abs(xf[:, 100]) + 0.5          # d = 100 has x > 0 for every token
     x = syn.bf16_from_f32(xf)
@@ -169,23 +172,50 @@ def test_router_near_ties_decided_in_fp64(oracle):
     w[12] = w[10]
     w[12, 100] -= 1
     bf = np.zeros(E, np.float32)
-    bf[[3, 7]] = 8.0
-    bf[[10, 11, 12]] = 4.0
+    bf[[3, 7]] = 16.0                                # logits are ~N(0, 1): gaps of >= 5 sigma
+    bf[[10, 11, 12]] = 8.0
     b = syn.bf16_from_f32(bf)
     got = _router_case(oracle, x, w, b, K)
     assert set(got[:, :2].ravel()) <= {3, 7}
 
 
+@pytest.mark.parametrize("B", [20, 144])
 @pytest.mark.parametrize("scale", [2.0 ** 66, 2.0 ** -70])
-def test_router_fp32_overflow_and_subnormal_products(oracle, scale):
+def test_router_fp32_overflow_and_subnormal_products(oracle, scale, B):
     """Products beyond the fp32 range (x, w ~ 2^66) or below its normal range
-    (~2^-140): the matrix-core pass yields non-finite or flushed sums, every
-    affected expert becomes a candidate and the fp64 pass ranks them."""
+    (~2^-140) keep the fp32-product semantics. In the two-pass router (B = 144)
+    the matrix-core sums are non-finite or flushed, so every affected expert
+    becomes a candidate and the exact pass ranks them."""
+    say(f"router fp32 range B={B} scale={scale}")
     rng = np.random.default_rng(6)
-    B, H, E, K = 20, 2880, 32, 4
+    H, E, K = 2880, 32, 4
     x = syn.bf16_from_f32((rng.standard_normal((B, H)) * scale).astype(np.float32))
     w = syn.bf16_from_f32((rng.standard_normal((E, H)) * scale).astype(np.float32))
     _router_case(oracle, x, w, None, K)
+
+
+@pytest.mark.parametrize("E,H,K", [(8, 64, 4), (40, 2880, 4), (128, 2880, 8), (17, 96, 1), (128, 3072, 4)])
+def test_router_two_pass_ties_nan_and_shapes(oracle, E, H, K):
+    """The two-pass router (B >= 128) on expert counts that are not multiples of
+    16, short and maximal rows, k = 1 and 8: random logits, experts with identical
+    rows (exact ties: the lower index wins), tokens with a NaN activation (NaN
+    logits rank last) and tokens whose logits are all equal."""
+    say(f"router two-pass E={E} H={H} K={K}")
+    rng = np.random.default_rng(E * 31 + H + K)
+    B = 137 if E <= 64 else 2048        # above 64 experts the two-pass router needs B * E >= 2^18
+    x = syn.bf16_from_f32(rng.standard_normal((B, H), dtype=np.float32))
+    w = syn.bf16_from_f32(rng.standard_normal((E, H), dtype=np.float32) * np.float32(0.05))
+    w[E - 1] = w[0]                      # tie between the first and last expert
+    if E > 4:
+        w[3] = w[2]
+    x[5, 7] = 0x7FC0                     # NaN activation
+    x[9] = 0                             # all logits equal (zero, no bias)
+    b = None if E % 2 else syn.bf16_from_f32(rng.standard_normal(E, dtype=np.float32) * np.float32(0.05))
+    if b is not None:
+        b[E - 1] = b[0]
+        if E > 4:
+            b[3] = b[2]
+    _router_case(oracle, x, w, b, K)
 
 
 @pytest.mark.parametrize("B,K,E,skew", [(1, 4, 32, False), (64, 4, 32, True), (4096, 4, 32, False),

@@ -700,12 +700,28 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
 
 // ---------------------------------------------------------------------------
 // Bucketing: counting sort of the B*k (token, slot) pairs by expert, stable in
-// pair id p = t*k + j. One workgroup of 1024 threads:
+// pair id p = t*k + j, by one workgroup of 1024 threads in one of two ways (both
+// give the same tables; each is the faster one where the launcher uses it).
+//
+// k_bucket_chunked (N <= 1024):
 //   1. histogram with LDS integer atomics (order-free, so deterministic);
 //   2. exclusive scans -> offsets[E+1] and the compact list of touched experts;
 //   3. pairs in chunks of 1024, in order: a lane's rank among equal keys of its
 //      wave comes from a ballot-based match, the wave's base from per-wave counts
 //      of the chunk; running per-expert totals carry across chunks.
+//
+// k_bucket_waves (larger N, where k_bucket_chunked spends four barriers per
+// chunk): wave w owns the contiguous pair range [w N / 16, (w + 1) N / 16),
+// walked in groups of 64:
+//   1. per-wave counts: in each group a lane finds the lanes with its key by
+//      ballots over the key bits, and the lowest of them adds their number to the
+//      wave's row of counts (no atomics, no barrier);
+//   2. counts summed over the waves, exclusive scans -> offsets[E+1], the
+//      compact list of touched experts and each wave's start within every
+//      expert (the counts of the waves before it);
+//   3. the same walk again: pair p goes to offsets[e] + the wave's start in e +
+//      the pairs of e the wave has placed so far + its rank among its group's
+//      lanes with key e.
 // Outputs perm (sorted position -> pair id), pos (pair id -> sorted position),
 // counts, offsets and the work-slot table slots[E]: slot a < #touched holds
 // {expert, tokens, first sorted position, 0} for the a-th touched expert
@@ -713,6 +729,8 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
 // Pairs whose expert id is outside [0, E) are dropped.
 // ---------------------------------------------------------------------------
 constexpr int kBucketThreads = 1024;
+constexpr int kBucketBlk = 16;  // groups of 64 pairs whose keys a wave loads at once
+static_assert(kBucketThreads / 64 == 16, "the bucketing scans assume 16 waves");
 
 // Exclusive prefix over the first n <= 1024 threads' values (later threads
 // contribute 0): shuffle scans inside each wave, then the wave totals; two
@@ -734,7 +752,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sbuf, int n) {
     return base + x - mine;
 }
 
-__global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __restrict__ idx, int N, int E,
+__global__ __launch_bounds__(kBucketThreads) void k_bucket_chunked(const int32_t* __restrict__ idx, int N, int E,
                                                            int32_t* __restrict__ counts,
                                                            int32_t* __restrict__ offsets,
                                                            int32_t* __restrict__ perm, int32_t* __restrict__ pos,
@@ -832,20 +850,168 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __rest
     }
 }
 
+__global__ __launch_bounds__(kBucketThreads) void k_bucket_waves(const int32_t* __restrict__ idx, int N, int E,
+                                                           int32_t* __restrict__ counts,
+                                                           int32_t* __restrict__ offsets,
+                                                           int32_t* __restrict__ perm, int32_t* __restrict__ pos,
+                                                           int4* __restrict__ slots, int32_t* __restrict__ n_slots,
+                                                           int32_t* __restrict__ tprefix, int tile_n,
+                                                           int4* __restrict__ passes, int32_t* __restrict__ n_passes) {
+    extern __shared__ int smem[];
+    int* cnt = smem;                   // [E] totals
+    int* off = cnt + E;                // [E] offsets
+    int* scan = off + E;               // [16] wave totals of the block scans
+    int* wcnt = scan + 16;             // [16][E] per-wave counts, then the waves' running starts
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nwaves = kBucketThreads / 64;
+
+    for (int i = tid; i < nwaves * E; i += kBucketThreads) wcnt[i] = 0;
+    __syncthreads();
+
+    int nbits = 1;
+    while ((1 << nbits) < E) ++nbits;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int pb = (int)((int64_t)wave * N / nwaves), pe = (int)((int64_t)(wave + 1) * N / nwaves);
+    int* mycnt = wcnt + wave * E;
+    // lanes of one group with the same valid key: `peers`; the lowest one leads
+    auto match = [&](int key) {
+        const bool valid = key >= 0 && key < E;
+        uint64_t peers = __ballot(valid);
+        if (!valid) peers = 0;
+        for (int bb = 0; bb < nbits; ++bb) {
+            const bool bit = (key >> bb) & 1;
+            const uint64_t m2 = __ballot(bit);
+            peers &= bit ? m2 : ~m2;
+        }
+        return peers;
+    };
+    // the keys of kBucketBlk groups at a time, all loads issued before the first use
+    int kk[kBucketBlk];
+    auto load_keys = [&](int base) {
+#pragma unroll
+        for (int i = 0; i < kBucketBlk; ++i) {
+            const int p = base + 64 * i + lane;
+            kk[i] = (p < pe) ? idx[p] : -1;
+        }
+    };
+    // ---- 1. per-wave counts ----
+    for (int base = pb; base < pe; base += 64 * kBucketBlk) {
+        load_keys(base);
+#pragma unroll
+        for (int i = 0; i < kBucketBlk; ++i) {
+            if (base + 64 * i >= pe) break;  // wave-uniform
+            const uint64_t peers = match(kk[i]);
+            if (peers && (peers & lt) == 0) mycnt[kk[i]] += __popcll(peers);
+        }
+    }
+    __syncthreads();
+    // counts -> starts of the waves within each expert, and the totals
+    if (E <= 64) {
+        // wave w, lane e: the rows before w read at once
+        int st = 0, tot = 0;
+        if (lane < E) {
+#pragma unroll
+            for (int w2 = 0; w2 < 16; ++w2) {
+                const int c = wcnt[w2 * E + lane];
+                st += (w2 < wave) ? c : 0;
+                tot += c;
+            }
+        }
+        __syncthreads();
+        if (lane < E) {
+            wcnt[wave * E + lane] = st;
+            if (wave == 0) cnt[lane] = tot;
+        }
+    } else {
+        for (int e = tid; e < E; e += kBucketThreads) {
+            int run = 0;
+            for (int w2 = 0; w2 < nwaves; ++w2) {
+                const int c = wcnt[w2 * E + e];
+                wcnt[w2 * E + e] = run;
+                run += c;
+            }
+            cnt[e] = run;
+        }
+    }
+    __syncthreads();
+
+    // offsets and the touched-expert list (E <= 1024: one expert per thread)
+    {
+        const int c = (tid < E) ? cnt[tid] : 0;  // E <= 1024
+        const int ex = block_excl_scan(c, scan, E);
+        const int na = block_excl_scan(c > 0 ? 1 : 0, scan, E);
+        if (tid < E) {
+            off[tid] = ex;
+            counts[tid] = c;
+            offsets[tid] = ex;
+            if (tid == E - 1) offsets[E] = ex + c;
+        }
+        if (slots) {
+            // touched experts take slots 0..#touched-1; the rest are cleared
+            const int ntouched = __syncthreads_count(tid < E && c > 0);
+            if (tid == 0 && n_slots) *n_slots = ntouched;
+            if (tid < E && c > 0) slots[na] = make_int4(tid, c, ex, 0);
+            if (tid >= ntouched && tid < E) slots[tid] = make_int4(0, 0, 0, 0);
+            if (tprefix) {
+                // exclusive prefix of token tiles over the slots (GEMM tile scheduling)
+                const int nt = (c + tile_n - 1) / tile_n;
+                const int tex = block_excl_scan(nt, scan, E);
+                if (tid < E && c > 0) tprefix[na] = tex;
+                if (tid == E - 1) tprefix[ntouched] = tex + nt;
+            }
+            if (passes) {
+                // each touched expert's sorted positions in chunks of kPassRows:
+                // {expert, tokens, first position, chunk index | chunk count << 16}
+                // (chunk counts stay below 2^16: the GEMV path has < 64 E pairs)
+                const int np = (c + kPassRows - 1) / kPassRows;
+                const int pex = block_excl_scan(np, scan, E);
+                if (tid < E)
+                    for (int t = 0; t < np; ++t)
+                        passes[pex + t] =
+                            make_int4(tid, min(kPassRows, c - t * kPassRows), ex + t * kPassRows, t | (np << 16));
+                if (tid == E - 1 && n_passes) *n_passes = pex + np;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 3. scatter, in the order of step 1 (one block of keys stays loaded) ----
+    for (int base = pb; base < pe; base += 64 * kBucketBlk) {
+        if (base != pb || pe - pb > 64 * kBucketBlk) load_keys(base);
+#pragma unroll
+        for (int i = 0; i < kBucketBlk; ++i) {
+            if (base + 64 * i >= pe) break;  // wave-uniform
+            const int key = kk[i], p = base + 64 * i + lane;
+            const uint64_t peers = match(key);
+            if (peers) {
+                const int q = off[key] + mycnt[key] + __popcll(peers & lt);
+                perm[q] = p;
+                if (pos) pos[p] = q;
+            }
+            __builtin_amdgcn_wave_barrier();  // every lane has read mycnt before the leaders advance it
+            if (peers && (peers & lt) == 0) mycnt[key] += __popcll(peers);
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
+// LDS of either bucketing kernel (k_bucket_chunked's is the larger)
 size_t bucket_smem_bytes(int E) { return sizeof(int) * ((size_t)3 * E + 16 + 16 * (size_t)E); }
+constexpr int kBucketChunkedMaxN = 1024;
 
 int bucket_launch(const void* idx, int N, int E, void* counts, void* offsets, void* perm, void* pos, void* slots,
                   void* n_slots, void* tprefix, int tile_n, void* passes, void* n_passes, hipStream_t stream) {
     static bool attr_set = false;
     const size_t smem = bucket_smem_bytes(E);
     if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)k_bucket, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)bucket_smem_bytes(kMaxExperts));
+        for (const void* k : {(const void*)k_bucket_chunked, (const void*)k_bucket_waves})
+            (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bucket_smem_bytes(kMaxExperts));
         attr_set = true;
     }
-    hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBucketThreads), smem, stream, (const int32_t*)idx, N, E,
-                       (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm, (int32_t*)pos, (int4*)slots,
-                       (int32_t*)n_slots, (int32_t*)tprefix, tile_n, (int4*)passes, (int32_t*)n_passes);
+    hipLaunchKernelGGL(N <= kBucketChunkedMaxN ? k_bucket_chunked : k_bucket_waves, dim3(1), dim3(kBucketThreads), smem,
+                       stream, (const int32_t*)idx, N, E, (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm,
+                       (int32_t*)pos, (int4*)slots, (int32_t*)n_slots, (int32_t*)tprefix, tile_n, (int4*)passes,
+                       (int32_t*)n_passes);
     return check_launch("bucket");
 }
 

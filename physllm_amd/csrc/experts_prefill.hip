@@ -448,7 +448,46 @@ __global__ __launch_bounds__(kG2Threads, 1) void k_mx_gemm2(GemvParams p, const 
         }
 
         // ---- epilogue of tile d ----
-        if (wave_rows) {
+        if (MODE == kModeGateUp) {
+            // h of the tile (128 tokens x 128 columns, bf16) goes through B buffer 1,
+            // free until the next tile's first k-step stores into it (after the
+            // barrier at the top of the loop): 16-byte chunk c of token row r at
+            // chunk c ^ (r & 15), so the fragment-order writes (16 token rows per
+            // instruction) are bank-conflict-free; then every 1 KiB store instruction
+            // writes 4 tokens' 256 contiguous bytes instead of 16 tokens' 16 bytes
+            uint32_t* ht = (uint32_t*)(bsm + kTN * kG2BRow);
+            if (wave_rows) {
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) {
+                    const int tl = wn * 64 + nt * 16 + m;  // token row of the tile
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        const float b0 = bf16_lo(bias_cur[mt].x), b1 = bf16_hi(bias_cur[mt].x);
+                        const float b2 = bf16_lo(bias_cur[mt].y), b3 = bf16_hi(bias_cur[mt].y);
+                        const f32x4_t c = acc[mt][nt];
+                        const float h0 = swiglu(c[0] + b0, c[1] + b1, p.alpha, p.limit);
+                        const float h1 = swiglu(c[2] + b2, c[3] + b3, p.alpha, p.limit);
+                        // h columns wm*32 + mt*8 + 2g, +1: word g of chunk wm*4 + mt
+                        ht[tl * 64 + (((wm * 4 + mt) ^ m) << 2) + g] = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
+                    }
+                }
+            }
+            __syncthreads();
+            const int I = p.R >> 1;
+            const int hc0 = d.row0 >> 1;  // the tile's first h column
+#pragma unroll
+            for (int u = 0; u < (kTN * 16) / kG2Threads; ++u) {
+                const int i = threadIdx.x + u * kG2Threads;
+                const int r = i >> 4, c = i & 15;  // token row, 16-byte chunk (8 h columns)
+                const int q = d.tok0 + r;
+                const int col = hc0 + c * 8;
+                // rows past R leave whole chunks past I (R and the tile rows are multiples of 16)
+                if (q < d.ne && col < I) {
+                    const uint4 v = ((const uint4*)ht)[r * 16 + (c ^ (r & 15))];
+                    *(uint4*)((uint16_t*)p.out + (size_t)(d.p0 + q) * I + col) = v;
+                }
+            }
+        } else if (wave_rows) {
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) {
                 const int q = d.tok0 + wn * 64 + nt * 16 + m;  // token column of this lane
@@ -461,20 +500,12 @@ __global__ __launch_bounds__(kG2Threads, 1) void k_mx_gemm2(GemvParams p, const 
                     const float b0 = bf16_lo(bias_cur[mt].x), b1 = bf16_hi(bias_cur[mt].x);
                     const float b2 = bf16_lo(bias_cur[mt].y), b3 = bf16_hi(bias_cur[mt].y);
                     const f32x4_t c = acc[mt][nt];
-                    if (MODE == kModeGateUp) {
-                        const float h0 = swiglu(c[0] + b0, c[1] + b1, p.alpha, p.limit);
-                        const float h1 = swiglu(c[2] + b2, c[3] + b3, p.alpha, p.limit);
-                        const int I = p.R >> 1;
-                        uint32_t* hout = (uint32_t*)((uint16_t*)p.out + (size_t)pp * I + (rr >> 1));
-                        *hout = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
-                    } else {
-                        float4 y;
-                        y.x = c[0] + b0;
-                        y.y = c[1] + b1;
-                        y.z = c[2] + b2;
-                        y.w = c[3] + b3;
-                        *(float4*)((float*)p.out + (size_t)pp * p.R + rr) = y;
-                    }
+                    float4 y;
+                    y.x = c[0] + b0;
+                    y.y = c[1] + b1;
+                    y.z = c[2] + b2;
+                    y.w = c[3] + b3;
+                    *(float4*)((float*)p.out + (size_t)pp * p.R + rr) = y;
                 }
             }
         }

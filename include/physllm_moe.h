@@ -1,9 +1,10 @@
 /*
  * physllm_moe.h — C ABI of the MI355X (gfx950) MXFP4 Mixture-of-Experts expert path.
  *
- * Drop-in for PhysLLM's MoE kernels. The five legacy launchers keep the exact
- * prototypes that crates/rocm-backend/src/ops.rs:554-594 binds, so the Rust
- * wrappers (ops.rs:597-696) link against this library unchanged. The extension
+ * Drop-in for PhysLLM's MoE kernels. The five MoE legacy launchers keep the exact
+ * prototypes that crates/rocm-backend/src/ops.rs:554-594 binds, and the RMSNorm and
+ * residual-add launchers those of ops.rs:315-332, so the Rust wrappers
+ * (ops.rs:366-384, :421-435, :597-696) link against this library unchanged. The extension
  * entry points carry what the legacy ABI cannot express: biases, MXFP4 expert
  * weights with E8M0 scales, batched and grouped tokens, and a caller-owned
  * workspace.
@@ -91,6 +92,21 @@ PHYSLLM_MOE_API void launch_moe_combine(const void* expert_outputs, const void* 
 PHYSLLM_MOE_API void launch_mxfp4_dequant(const void* packed_data, const void* scales, void* output, int numel,
                           int block_size, void* stream);
 
+/* Replaces kernels/rms_norm_gpu.hip:36-45 (bound at crates/rocm-backend/src/ops.rs:315-319,
+ * wrapped at ops.rs:366-384 and called before the router at moe.rs:239-244).
+ * input [batch_size,hidden_dim] bf16, weight [hidden_dim] bf16, output like input
+ * (may equal input). Per row: sum of v*v in the reference kernel's order (256
+ * strided fp32 partials, one fma per element, then its shared-memory tree),
+ * rms = sqrtf(sum / hidden_dim + eps), output = bf16((v / rms) * weight).
+ * Bit-identical to that order for bf16 data. */
+PHYSLLM_MOE_API void launch_rms_norm(const void* input, const void* weight, void* output, int batch_size,
+                     int hidden_dim, float eps, void* stream);
+
+/* Replaces kernels/residual_add.hip:12-19 (bound at ops.rs:329-332, wrapped at
+ * ops.rs:421-435, called after the combine at moe.rs:310-311).
+ * output[i] = bf16(output[i] + residual[i]) in fp32, for i < size (bf16 data). */
+PHYSLLM_MOE_API void launch_residual_add(void* output, const void* residual, int size, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Extension entry points (no reference counterpart; they carry the benchmark */
 /* semantics: biases, MXFP4 experts, batching). Callers: the bench/test       */
@@ -155,6 +171,21 @@ PHYSLLM_MOE_API int physllm_moe_stage_down(const physllm_moe_config* cfg, const 
                            int batch, void* workspace, size_t workspace_bytes, void* stream);
 PHYSLLM_MOE_API int physllm_moe_stage_combine(const physllm_moe_config* cfg, int batch, void* out,
                               const void* topk_w, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* Workspace bytes physllm_moe_block_forward needs for `batch` tokens (the layer's
+ * workspace plus the normalised activations). */
+PHYSLLM_MOE_API size_t physllm_moe_block_workspace_bytes(const physllm_moe_config* cfg, int batch);
+
+/* The MoE sub-layer of a transformer block, crates/llm-core/src/moe.rs:238-313:
+ *   h = rms_norm(x, norm_w, eps)   (moe.rs:239-244, kernels/rms_norm_gpu.hip:4-31)
+ *   m = physllm_moe_layer_forward(h)                    (moe.rs:246-307)
+ *   out = bf16(m + x)              (moe.rs:310-311, kernels/residual_add.hip:4-10)
+ * x, out [batch,H] bf16; norm_w [H] bf16. out may equal x (in place, as the
+ * reference updates its residual buffer). topk_idx / topk_w as for the layer. */
+PHYSLLM_MOE_API int physllm_moe_block_forward(const physllm_moe_config* cfg, const physllm_moe_weights* w,
+                              const void* x, const void* norm_w, float eps, int batch, void* out,
+                              void* topk_idx, void* topk_w, void* workspace, size_t workspace_bytes,
                               void* stream);
 
 /* Router with bias: x [batch,H] bf16, router_w [E,H] bf16, router_b [E] bf16

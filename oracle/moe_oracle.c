@@ -10,6 +10,9 @@
  *   gate_up : fp32 serial sum, + bias (fp32), clamped SwiGLU in fp32, -> bf16
  *   down    : fp32 serial sum, + bias (fp32), kept fp32
  *   combine : fp32 fmaf over k in k order, -> bf16 once
+ *   rms_norm: fp32 256-way strided partial sums of squares (fmaf) + the kernel's tree,
+ *             sqrtf(sum/H + eps), (v / rms) * weight -> bf16
+ *   residual: bf16(float(a) + float(b))
  * Built with -ffp-contract=off so that "serial fp32 sum" means one rounding
  * per multiply and one per add.
  *
@@ -25,6 +28,13 @@
  *   or_moe_layer / or_moe_experts : float64 numpy brute force on tiny shapes
  *       using weights decoded by an independent decoder; committed golden fixture.
  *   or_legacy_* : float64 numpy brute force.
+ *   or_rms_norm : closed forms (constant rows, a single nonzero element, power-of-two
+ *       scaling of a row with eps = 0 leaves it unchanged), the float64 brute force
+ *       within the fp32 error of the 256-way sum, and the summation order itself
+ *       (a row built so that another order rounds differently).
+ *   or_residual_add : exact float64 sums rounded to bf16 by an independent
+ *       (numpy) rounding.
+ *   or_moe_block : composition of the pinned functions above.
  */
 #include "moe_oracle.h"
 
@@ -401,6 +411,63 @@ int or_moe_layer(const or_moe_cfg* cfg, const or_moe_weights* w, const uint16_t*
     if (!idx) free(ix);
     if (!wts) free(ws);
     return rc;
+}
+
+/* ------------------------------------------------------------------------- */
+/* the steps either side of the layer: rms_norm before, residual add after      */
+/* ------------------------------------------------------------------------- */
+
+/* kernels/rms_norm_gpu.hip:4-31 with bf16 data: per row, thread j of the
+ * 256-thread block sums v*v over i = j, j + 256, ... in order (:11-15); the block
+ * adds the 256 partials by its shared-memory tree, s = 128, 64, ..., 1:
+ * p[j] += p[j + s] for j < s (:18-21); rms = sqrtf(p[0] / H + eps) (:24);
+ * out[i] = round((v / rms) * weight[i]) (:30). fp32 throughout. `tsum += v * v` (:14)
+ * is one fmaf: hipcc contracts it so under HIP's default -ffp-contract=fast-honor-pragmas.
+ * For bf16 v the product is exact in fp32 unless |v| < 2^-63, so only rows that small
+ * can tell the fused from the unfused form. */
+void or_rms_norm(const uint16_t* x, const uint16_t* wt, uint16_t* out, int B, int H, float eps) {
+    for (int b = 0; b < B; ++b) {
+        const uint16_t* row = x + (size_t)b * H;
+        float p[256];
+        for (int j = 0; j < 256; ++j) {
+            float t = 0.0f;
+            for (int i = j; i < H; i += 256) {
+                const float v = or_bf16_to_f32(row[i]);
+                t = fmaf(v, v, t);
+            }
+            p[j] = t;
+        }
+        for (int s2 = 128; s2 > 0; s2 >>= 1)
+            for (int j = 0; j < s2; ++j) p[j] = p[j] + p[j + s2];
+        const float rms = sqrtf(p[0] / (float)H + eps);
+        for (int i = 0; i < H; ++i) {
+            const float v = or_bf16_to_f32(row[i]);
+            const float q = v / rms;
+            out[(size_t)b * H + i] = or_f32_to_bf16(q * or_bf16_to_f32(wt[i]));
+        }
+    }
+}
+
+/* kernels/residual_add.hip:4-10 with bf16 data: out[i] = round(out[i] + res[i]) in fp32. */
+void or_residual_add(uint16_t* out, const uint16_t* res, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = or_f32_to_bf16(or_bf16_to_f32(out[i]) + or_bf16_to_f32(res[i]));
+}
+
+/* The MoE sub-layer of crates/llm-core/src/moe.rs:238-313: h = rms_norm(x) (:240-244),
+ * the layer (or_moe_layer, :246-307), then the residual add into the hidden state
+ * (:310): out = round(moe(h) + x). */
+int or_moe_block(const or_moe_cfg* cfg, const or_moe_weights* w, const uint16_t* x, const uint16_t* norm_w,
+                 float eps, int B, uint16_t* out, int32_t* idx, float* wts, int nthreads) {
+    const int H = cfg->hidden;
+    if (B < 0) return -1;
+    if (B == 0) return 0;
+    uint16_t* h = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)B * H);
+    or_rms_norm(x, norm_w, h, B, H, eps);
+    const int rc = or_moe_layer(cfg, w, h, B, out, idx, wts, NULL, NULL, nthreads);
+    free(h);
+    if (rc) return rc;
+    or_residual_add(out, x, (size_t)B * H);
+    return 0;
 }
 
 /* ------------------------------------------------------------------------- */

@@ -92,6 +92,13 @@ void or_legacy_expert_down(const uint16_t* inter, const uint16_t* wd, uint16_t* 
                            int H, int I);
 void or_legacy_combine(const uint16_t* y, const float* w, uint16_t* out, int H, int K);
 
+/* the steps either side of the layer (kernels/rms_norm_gpu.hip, kernels/residual_add.hip)
+ * and the sub-layer they bracket (crates/llm-core/src/moe.rs:238-313) */
+void or_rms_norm(const uint16_t* x, const uint16_t* wt, uint16_t* out, int B, int H, float eps);
+void or_residual_add(uint16_t* out, const uint16_t* res, size_t n);
+int or_moe_block(const or_moe_cfg* cfg, const or_moe_weights* w, const uint16_t* x, const uint16_t* norm_w,
+                 float eps, int B, uint16_t* out, int32_t* idx, float* wts, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,10 @@ def lib():
         L.or_legacy_expert_silu.argtypes, L.or_legacy_expert_silu.restype = [P, P, P, P, I, I], None
         L.or_legacy_expert_down.argtypes, L.or_legacy_expert_down.restype = [P, P, P, I, I], None
         L.or_legacy_combine.argtypes, L.or_legacy_combine.restype = [P, P, P, I, I], None
+        L.or_rms_norm.argtypes, L.or_rms_norm.restype = [P, P, P, I, I, F], None
+        L.or_residual_add.argtypes, L.or_residual_add.restype = [P, P, ctypes.c_size_t], None
+        L.or_moe_block.argtypes = [ctypes.POINTER(_Cfg), ctypes.POINTER(_W), P, P, F, I, P, P, P, I]
+        L.or_moe_block.restype = I
         _lib = L
     return _lib
 
@@ -226,3 +230,40 @@ def legacy_combine(y, w):
     out = np.empty(H, dtype=np.uint16)
     lib().or_legacy_combine(_p(y), _p(w), _p(out), H, K)
     return out
+
+
+def rms_norm(x, weight, eps: float):
+    """kernels/rms_norm_gpu.hip:4-31 with bf16 data: x [B,H], weight [H] bf16 bits."""
+    x, weight = _c(x, np.uint16), _c(weight, np.uint16)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    B, H = x.shape
+    out = np.empty((B, H), dtype=np.uint16)
+    lib().or_rms_norm(_p(x), _p(weight), _p(out), B, H, float(eps))
+    return out
+
+
+def residual_add(out, res):
+    """kernels/residual_add.hip:4-10 with bf16 data: returns bf16(out + res)."""
+    o = _c(out, np.uint16).copy()
+    r = _c(res, np.uint16)
+    lib().or_residual_add(_p(o), _p(r), o.size)
+    return o
+
+
+def moe_block(layer, x, norm_w, eps: float, nthreads: int = 0):
+    """crates/llm-core/src/moe.rs:238-313: rms_norm -> MoE layer -> residual add.
+    Returns dict(out, idx, wts)."""
+    x = _c(x, np.uint16)
+    norm_w = _c(norm_w, np.uint16)
+    B = x.shape[0]
+    cfg, w, keep = _cfg_w(layer)
+    K, H = layer.top_k, layer.hidden
+    out = np.empty((B, H), dtype=np.uint16)
+    idx = np.empty((B, K), dtype=np.int32)
+    wts = np.empty((B, K), dtype=np.float32)
+    rc = lib().or_moe_block(ctypes.byref(cfg), ctypes.byref(w), _p(x), _p(norm_w), float(eps), B, _p(out),
+                            _p(idx), _p(wts), nthreads or default_threads())
+    if rc != 0:
+        raise ValueError(f"or_moe_block rc={rc}")
+    return dict(out=out, idx=idx, wts=wts)

@@ -57,9 +57,14 @@ def lib() -> ctypes.CDLL:
         "launch_moe_expert_down": ([P, P, P, I, I, P], None),
         "launch_moe_combine": ([P, P, P, I, I, P], None),
         "launch_mxfp4_dequant": ([P, P, P, I, I, P], None),
+        "launch_rms_norm": ([P, P, P, I, I, ctypes.c_float, P], None),
+        "launch_residual_add": ([P, P, I, P], None),
         "physllm_moe_workspace_bytes": ([ctypes.POINTER(MoEConfig), I], SZ),
         "physllm_moe_layer_forward": ([ctypes.POINTER(MoEConfig), ctypes.POINTER(MoEWeights), P, I, P,
                                        P, P, P, SZ, P], I),
+        "physllm_moe_block_workspace_bytes": ([ctypes.POINTER(MoEConfig), I], SZ),
+        "physllm_moe_block_forward": ([ctypes.POINTER(MoEConfig), ctypes.POINTER(MoEWeights), P, P,
+                                       ctypes.c_float, I, P, P, P, P, SZ, P], I),
         "physllm_moe_stage_route": ([ctypes.POINTER(MoEConfig), ctypes.POINTER(MoEWeights), P, I, P, P, P,
                                      SZ, P], I),
         "physllm_moe_stage_gate_up": ([ctypes.POINTER(MoEConfig), ctypes.POINTER(MoEWeights), P, I, P, SZ,

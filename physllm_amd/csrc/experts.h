@@ -37,8 +37,13 @@ constexpr int kMaxSplit = 4;
 constexpr int kPassRows = 16;  // tokens per pass-table entry (the MFMA's N)
 
 int gemv_launch(int mode, const GemvParams& p, int max_slots, int max_tokens, hipStream_t stream);
+// out [B,H] = bf16(sum over k of w * y), then, when res is not null,
+// out = bf16(out + res) (the residual add after the layer; res may equal out).
 int combine_launch(const float* y, int nsplit, size_t split_stride, const int32_t* pos, const float* wts,
-                   uint16_t* out, int B, int H, int K, hipStream_t stream);
+                   uint16_t* out, const uint16_t* res, int B, int H, int K, hipStream_t stream);
+// RMSNorm of B rows of H bf16 values (out may equal x) and the bf16 residual add.
+int rms_norm_launch(const void* x, const void* w, void* out, int B, int H, float eps, hipStream_t stream);
+int residual_add_launch(void* out, const void* res, int64_t n, hipStream_t stream);
 // Counting sort of the routed pairs by expert. Optional outputs (nullable): the
 // slot table and its count, the per-slot prefix of tile_n-token tiles, and the
 // pass table (chunks of kPassRows tokens) with its count.

@@ -614,8 +614,8 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
 // the sum of the split partials, added in split order first. Each lane handles 4
 // consecutive d.
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, const int32_t* __restrict__ pos,
-                                                 const float* __restrict__ wts, uint16_t* __restrict__ out, int H,
-                                                 int K, int nsplit, size_t split_stride) {
+                                                 const float* __restrict__ wts, uint16_t* out, const uint16_t* res,
+                                                 int H, int K, int nsplit, size_t split_stride) {
     const int t = blockIdx.y;
     const int d4 = blockIdx.x * 256 + threadIdx.x;
     if (d4 * 4 >= H) return;
@@ -639,6 +639,13 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, co
     uint2 o;
     o.x = f32_to_bf16(acc.x) | (f32_to_bf16(acc.y) << 16);
     o.y = f32_to_bf16(acc.z) | (f32_to_bf16(acc.w) << 16);
+    if (res) {
+        // the layer's output is a bf16 tensor first, then the residual add
+        // (crates/llm-core/src/moe.rs:310-311, kernels/residual_add.hip:9)
+        const uint2 r = ((const uint2*)(res + (size_t)t * H))[d4];
+        o.x = f32_to_bf16(bf16_lo(o.x) + bf16_lo(r.x)) | (f32_to_bf16(bf16_hi(o.x) + bf16_hi(r.x)) << 16);
+        o.y = f32_to_bf16(bf16_lo(o.y) + bf16_lo(r.y)) | (f32_to_bf16(bf16_hi(o.y) + bf16_hi(r.y)) << 16);
+    }
     ((uint2*)(out + (size_t)t * H))[d4] = o;
 }
 
@@ -715,9 +722,9 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
 }
 
 int combine_launch(const float* y, int nsplit, size_t split_stride, const int32_t* pos, const float* wts,
-                   uint16_t* out, int B, int H, int K, hipStream_t stream) {
+                   uint16_t* out, const uint16_t* res, int B, int H, int K, hipStream_t stream) {
     dim3 grid((H / 4 + 255) / 256, B);
-    hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, stream, y, pos, wts, out, H, K, nsplit, split_stride);
+    hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, stream, y, pos, wts, out, res, H, K, nsplit, split_stride);
     return check_launch("combine");
 }
 

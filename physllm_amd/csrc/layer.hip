@@ -136,9 +136,10 @@ extern "C" size_t physllm_moe_workspace_bytes(const physllm_moe_config* cfg, int
 // 0 route (router + bucketing), 1 gate_up (+ SwiGLU), 2 down, 3 combine.
 enum { kStageRoute = 1, kStageGateUp = 2, kStageDown = 4, kStageCombine = 8, kStageAll = 15 };
 
+// `residual` (nullable) is added to the combined output: out = bf16(out + residual).
 static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* w, const void* x, int batch,
                       void* out, void* topk_idx, void* topk_w, void* workspace, size_t workspace_bytes,
-                      hipStream_t s, int stages) {
+                      hipStream_t s, int stages, const void* residual = nullptr) {
     int rc = validate(cfg, batch);
     if (rc) return rc;
     if (batch == 0) return ok();
@@ -211,8 +212,8 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
         if (rc) return rc;
     }
     if (stages & kStageCombine) {
-        if ((rc = combine_launch(ws.y, ws.split, (size_t)N * c.hidden, ws.pos, wts, (uint16_t*)out, batch, c.hidden,
-                                 c.top_k, s)))
+        if ((rc = combine_launch(ws.y, ws.split, (size_t)N * c.hidden, ws.pos, wts, (uint16_t*)out,
+                                 (const uint16_t*)residual, batch, c.hidden, c.top_k, s)))
             return rc;
     }
     return ok();
@@ -248,4 +249,38 @@ extern "C" int physllm_moe_stage_combine(const physllm_moe_config* cfg, int batc
                                          void* workspace, size_t workspace_bytes, void* stream) {
     return run_stages(cfg, nullptr, nullptr, batch, out, nullptr, (void*)topk_w, workspace, workspace_bytes,
                       (hipStream_t)stream, kStageCombine);
+}
+
+// The MoE sub-layer of a transformer block (crates/llm-core/src/moe.rs:238-313):
+// h = rms_norm(x) into the tail of the workspace, the layer on h, and the residual
+// add of x fused into the combine. out may equal x (the reference updates its
+// residual buffer in place): x is read by the norm and, per element, by the
+// combine thread that then writes that element.
+static size_t block_norm_bytes(const physllm_moe_config& c, int batch) {
+    return align256((size_t)batch * c.hidden * 2);
+}
+
+extern "C" size_t physllm_moe_block_workspace_bytes(const physllm_moe_config* cfg, int batch) {
+    if (validate(cfg, batch) != PHYSLLM_MOE_OK) return 0;
+    ok();
+    return carve(*cfg, batch, nullptr).bytes + block_norm_bytes(*cfg, batch);
+}
+
+extern "C" int physllm_moe_block_forward(const physllm_moe_config* cfg, const physllm_moe_weights* w,
+                                         const void* x, const void* norm_w, float eps, int batch, void* out,
+                                         void* topk_idx, void* topk_w, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+    int rc = validate(cfg, batch);
+    if (rc) return rc;
+    if (batch == 0) return ok();
+    if (!x || !norm_w || !out) return set_error(PHYSLLM_MOE_EINVAL, "block: null x, norm_w or out");
+    const size_t lay = carve(*cfg, batch, nullptr).bytes;
+    if (!workspace || workspace_bytes < lay + block_norm_bytes(*cfg, batch))
+        return set_error(PHYSLLM_MOE_EWORKSPACE, "block: workspace too small");
+    if (!w || !w->router_w || !w->gate_up_blocks || !w->gate_up_scales || !w->down_blocks || !w->down_scales)
+        return set_error(PHYSLLM_MOE_EINVAL, "layer: null weight pointer");
+    const hipStream_t s = (hipStream_t)stream;
+    void* h = (char*)workspace + lay;
+    if ((rc = rms_norm_launch(x, norm_w, h, batch, cfg->hidden, eps, s))) return rc;
+    return run_stages(cfg, w, h, batch, out, topk_idx, topk_w, workspace, lay, s, kStageAll, x);
 }

@@ -92,6 +92,22 @@ def mxfp4_dequant_gpu(dev: GpuDevice, packed, scales, output, block_size: int) -
     dev.synchronise()
 
 
+def rms_norm_gpu(dev: GpuDevice, inp, weight, output, eps: float) -> None:
+    """ops.rs:366-384: batch = input.rows(), hidden_dim = input.cols()."""
+    batch, hidden_dim = _rows_cols(inp)
+    lib().launch_rms_norm(_ptr(inp), _ptr(weight), _ptr(output), batch, hidden_dim, float(eps),
+                          dev.raw_stream())
+    check()
+    dev.synchronise()
+
+
+def residual_add_gpu(dev: GpuDevice, output, residual) -> None:
+    """ops.rs:421-435: output += residual over output.numel() elements."""
+    lib().launch_residual_add(_ptr(output), _ptr(residual), output.numel(), dev.raw_stream())
+    check()
+    dev.synchronise()
+
+
 # ---- extension wrappers ----------------------------------------------------------
 
 def mxfp4_dequant(packed, scales, output, stream: int = 0) -> None:
@@ -167,6 +183,37 @@ class DeviceMoELayer:
                                              _ptr(x), B, _ptr(out), _ptr(topk_idx), _ptr(topk_w),
                                              _ptr(workspace), workspace.numel() * workspace.element_size(), s)
         check(rc)
+
+
+    def block_workspace_bytes(self, batch: int) -> int:
+        n = lib().physllm_moe_block_workspace_bytes(ctypes.byref(self.cfg), batch)
+        if n == 0 and batch > 0:
+            check(capi.last_error()[0] or capi.PHYSLLM_MOE_EINVAL)
+        return int(n)
+
+    def block_forward(self, x: torch.Tensor, norm_w: torch.Tensor, eps: float, out: torch.Tensor,
+                      workspace: torch.Tensor, topk_idx: Optional[torch.Tensor] = None,
+                      topk_w: Optional[torch.Tensor] = None, stream: Optional[int] = None) -> None:
+        """moe.rs:238-313: out = x + layer(rms_norm(x)); out may be x itself."""
+        B = x.shape[0]
+        s = torch.cuda.current_stream().cuda_stream if stream is None else stream
+        rc = lib().physllm_moe_block_forward(ctypes.byref(self.cfg), ctypes.byref(self.weights), _ptr(x),
+                                             _ptr(norm_w), float(eps), B, _ptr(out), _ptr(topk_idx),
+                                             _ptr(topk_w), _ptr(workspace),
+                                             workspace.numel() * workspace.element_size(), s)
+        check(rc)
+
+
+def moe_block_forward(dlayer: DeviceMoELayer, x: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                      return_routing: bool = False):
+    """Allocating convenience wrapper of the block: returns out [B,H] (int16 bf16 bits) [, idx, w]."""
+    B = x.shape[0]
+    out = torch.empty((B, dlayer.hidden), dtype=torch.int16, device=x.device)
+    ws = torch.empty(max(dlayer.block_workspace_bytes(B), 1), dtype=torch.uint8, device=x.device)
+    idx = torch.empty((B, dlayer.top_k), dtype=torch.int32, device=x.device) if return_routing else None
+    w = torch.empty((B, dlayer.top_k), dtype=torch.float32, device=x.device) if return_routing else None
+    dlayer.block_forward(x, norm_w, eps, out, ws, idx, w)
+    return (out, idx, w) if return_routing else out
 
 
 def moe_layer_forward(dlayer: DeviceMoELayer, x: torch.Tensor, return_routing: bool = False):

@@ -142,6 +142,81 @@ def moe_layer_f64(layer, x_bits: np.ndarray, round_h: bool = True):
     return out, idx, w
 
 
+def rms_norm_f64(x_bits: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarray:
+    """Float64 RMSNorm: x / sqrt(mean(x^2) + eps) * w, per row (no rounding)."""
+    x = bf16_bits_to_f64(x_bits)
+    w = bf16_bits_to_f64(w_bits)
+    rms = np.sqrt((x * x).mean(axis=-1, keepdims=True) + np.float64(np.float32(eps)))
+    return x / rms * w
+
+
+def bf16_ulp_distance(a_bits, b_bits) -> np.ndarray:
+    """Distance in representable bf16 steps between finite bf16 values (sign aware)."""
+    def key(u):
+        u = np.asarray(u, dtype=np.uint16).astype(np.int64)
+        return np.where(u & 0x8000, -(u & 0x7FFF), u)
+    return np.abs(key(a_bits) - key(b_bits))
+
+
+def f32_of_bits(u) -> np.ndarray:
+    return (np.asarray(u, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bits_of_f32_rne(f) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even (finite inputs)."""
+    u = np.asarray(f, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def sum_sq_f32(v: np.ndarray, order: str):
+    """Sum of squares of a float32 row in float32, in one of two orders:
+    'tree' = kernels/rms_norm_gpu.hip:11-21 (256 strided partials, then
+    p[:s] += p[s:2s] for s = 128..1), written as array operations;
+    'serial' = left to right (a plausible mistake)."""
+    sq = v * v  # exact for bf16 inputs of normal magnitude
+    if order == "serial":
+        t = np.float32(0)
+        for q in sq:
+            t = np.float32(t + q)
+        return t
+    n = -(-v.size // 256) * 256
+    cols = np.zeros(n, dtype=np.float32)
+    cols[: v.size] = sq
+    p = np.zeros(256, dtype=np.float32)
+    for r in cols.reshape(-1, 256):
+        p = p + r
+    s = 128
+    while s:
+        p[:s] = p[:s] + p[s:2 * s]
+        s //= 2
+    return p[0]
+
+
+def rms_order_sensitive_row(H: int, seed: int):
+    """A bf16 row x and weights w (all 1.0 but w[i]) for which RMSNorm (eps = 0) gives
+    a different output bit at i when the sum of squares is taken left to right
+    instead of in the tree order. Returns (x, w, i, bits_tree, bits_serial)."""
+    rng = np.random.default_rng(seed)
+    wall = np.arange(0x0080, 0x7000, dtype=np.uint16)  # positive normal bf16 below 2^97
+    wf = f32_of_bits(wall)
+    for _ in range(50):
+        x = bits_of_f32_rne(rng.standard_normal(H).astype(np.float32))
+        v = f32_of_bits(x)
+        r_tree = np.sqrt(np.float32(sum_sq_f32(v, "tree") / np.float32(H)))
+        r_ser = np.sqrt(np.float32(sum_sq_f32(v, "serial") / np.float32(H)))
+        if r_tree == r_ser:
+            continue
+        for i in range(H):
+            b1 = bits_of_f32_rne((v[i] / r_tree) * wf)
+            b2 = bits_of_f32_rne((v[i] / r_ser) * wf)
+            hit = np.flatnonzero(b1 != b2)
+            if hit.size:
+                w = np.full(H, 0x3F80, dtype=np.uint16)
+                w[i] = wall[hit[0]]
+                return x, w, i, b1[hit[0]], b2[hit[0]]
+    raise RuntimeError("no order-sensitive row found")
+
+
 def rel_l2(a, b) -> float:
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)

@@ -1,5 +1,6 @@
 """C-ABI checks that need no GPU: the library loads, exports exactly what the
-header declares (with the legacy prototypes of crates/rocm-backend/src/ops.rs:554-594),
+header declares (with the legacy prototypes of crates/rocm-backend/src/ops.rs:315-332
+and :554-594),
 and rejects bad arguments on the host before any HIP call."""
 import ctypes
 import re
@@ -8,7 +9,7 @@ import subprocess
 from physllm_amd import capi
 
 LEGACY = ["launch_moe_router", "launch_moe_expert_silu", "launch_moe_expert_down",
-          "launch_moe_combine", "launch_mxfp4_dequant"]
+          "launch_moe_combine", "launch_mxfp4_dequant", "launch_rms_norm", "launch_residual_add"]
 
 
 def test_library_exports_every_header_symbol():
@@ -36,6 +37,9 @@ def test_legacy_prototypes_match_rust_ffi():
         "launch_moe_expert_down": ["const void*", "const void*", "void*", "int", "int", "void*"],
         "launch_moe_combine": ["const void*", "const void*", "void*", "int", "int", "void*"],
         "launch_mxfp4_dequant": ["const void*", "const void*", "void*", "int", "int", "void*"],
+        # ops.rs:315-319 and :329-332
+        "launch_rms_norm": ["const void*", "const void*", "void*", "int", "int", "float", "void*"],
+        "launch_residual_add": ["void*", "const void*", "int", "void*"],
     }
     for name, types in expect.items():
         m = re.search(r"void\s+" + name + r"\s*\(([^)]*)\)", hdr)
@@ -92,3 +96,44 @@ def test_layer_rejects_bad_arguments_on_host():
     assert L.physllm_moe_last_error() == capi.PHYSLLM_MOE_EINVAL
     L.launch_moe_combine(None, None, None, 2880, 4, None)
     assert L.physllm_moe_last_error() == capi.PHYSLLM_MOE_EINVAL
+
+
+def test_block_workspace_and_validation_without_gpu():
+    """The block entry (moe.rs:238-313) needs the layer's workspace plus B*H bf16
+    for the normalised activations, and checks its arguments before any launch."""
+    L = capi.lib()
+    cfg = capi.MoEConfig(2880, 2880, 32, 4, 1.702, 7.0)
+    for B in (1, 7, 64, 4096):
+        lay = L.physllm_moe_workspace_bytes(ctypes.byref(cfg), B)
+        blk = L.physllm_moe_block_workspace_bytes(ctypes.byref(cfg), B)
+        assert blk == lay + ((B * 2880 * 2 + 255) // 256) * 256
+    bad = capi.MoEConfig(2880, 2880, 32, 0, 1.702, 7.0)
+    assert L.physllm_moe_block_workspace_bytes(ctypes.byref(bad), 1) == 0
+    assert L.physllm_moe_last_error() == capi.PHYSLLM_MOE_EINVAL
+    fake = ctypes.c_void_p(0x1000)
+    w = capi.MoEWeights(fake, None, fake, fake, None, fake, fake, None)
+    args = lambda x, nw, B, out, ws, n: (ctypes.byref(cfg), ctypes.byref(w), x, nw, 1e-5, B, out, None, None,
+                                         ws, n, None)
+    assert L.physllm_moe_block_forward(*args(None, None, 0, None, None, 0)) == capi.PHYSLLM_MOE_OK
+    assert L.physllm_moe_block_forward(*args(fake, fake, -1, fake, fake, 1 << 30)) == capi.PHYSLLM_MOE_EINVAL
+    assert L.physllm_moe_block_forward(*args(fake, None, 2, fake, fake, 1 << 30)) == capi.PHYSLLM_MOE_EINVAL
+    assert b"norm_w" in L.physllm_moe_last_error_message()
+    need = L.physllm_moe_block_workspace_bytes(ctypes.byref(cfg), 2)
+    assert L.physllm_moe_block_forward(*args(fake, fake, 2, fake, fake, need - 1)) == capi.PHYSLLM_MOE_EWORKSPACE
+    w0 = capi.MoEWeights()
+    rc = L.physllm_moe_block_forward(ctypes.byref(cfg), ctypes.byref(w0), fake, fake, 1e-5, 2, fake, None, None,
+                                     fake, need, None)
+    assert rc == capi.PHYSLLM_MOE_EINVAL and b"weight" in L.physllm_moe_last_error_message()
+    # legacy launchers: bad sizes and null pointers are refused, empty work is a no-op
+    L.launch_rms_norm(fake, fake, fake, 1, 0, 1e-5, None)
+    assert L.physllm_moe_last_error() == capi.PHYSLLM_MOE_EINVAL
+    L.launch_rms_norm(fake, None, fake, 1, 2880, 1e-5, None)
+    assert L.physllm_moe_last_error() == capi.PHYSLLM_MOE_EINVAL
+    L.launch_rms_norm(fake, fake, fake, 0, 2880, 1e-5, None)
+    assert L.physllm_moe_last_error() == 0
+    L.launch_residual_add(fake, fake, -1, None)
+    assert L.physllm_moe_last_error() == capi.PHYSLLM_MOE_EINVAL
+    L.launch_residual_add(None, fake, 8, None)
+    assert L.physllm_moe_last_error() == capi.PHYSLLM_MOE_EINVAL
+    L.launch_residual_add(fake, fake, 0, None)
+    assert L.physllm_moe_last_error() == 0

@@ -262,3 +262,113 @@ def test_synthetic_distributions():
     # per-expert algorithmic bytes for the GPT-OSS shape (13,236,480 B)
     big = syn.MoELayer(2880, 2880, 1, 4, *[None] * 8)
     assert big.expert_bytes == 13_236_480
+
+
+# ---- rms_norm before the layer, residual add after it ------------------------------
+
+def test_rms_norm_closed_forms(oracle):
+    H = 2880
+    # a constant row c: sum = H c^2 exactly, rms = |c|, out = sign(c) * w
+    w = np.full(H, 0x3F80, dtype=np.uint16)                      # 1.0
+    for c, want in ((0x3FC0, 0x3F80), (0xBFC0, 0xBF80), (0x4300, 0x3F80)):   # 1.5, -1.5, 128
+        out = oracle.rms_norm(np.full((1, H), c, dtype=np.uint16), w, 0.0)
+        assert np.all(out == want), (hex(c), np.unique(out))
+    wv = np.arange(H, dtype=np.uint16) % 200 + 0x3C00               # assorted weights
+    out = oracle.rms_norm(np.full((1, H), 0x3FC0, dtype=np.uint16), wv, 0.0)
+    assert np.array_equal(out[0], wv)
+    # one nonzero element a in a row of 64: rms = |a| / 8, out[i] = 8 sign(a) w[i], zeros elsewhere
+    x = np.zeros((2, 64), dtype=np.uint16)
+    x[0, 5] = 0x4049            # 3.140625
+    x[1, 63] = 0xC2F6           # -123
+    out = oracle.rms_norm(x, np.full(64, 0x3F80, dtype=np.uint16), 0.0)
+    assert out[0, 5] == 0x4100 and out[1, 63] == 0xC100           # +8, -8
+    assert np.all(np.delete(out[0], 5) == 0) and np.all(np.delete(out[1], 63) == 0)
+    # a zero row: 0 / sqrt(eps) keeps the zeros (and their signs); with eps = 0 it is 0/0
+    z = np.zeros((1, 300), dtype=np.uint16)
+    z[0, 7] = 0x8000
+    out = oracle.rms_norm(z, np.full(300, 0x3F80, dtype=np.uint16), 1e-5)
+    assert np.all((out[0] & 0x7FFF) == 0) and out[0, 7] == 0x8000 and out[0, 6] == 0
+    out = oracle.rms_norm(z, np.full(300, 0x3F80, dtype=np.uint16), 0.0)
+    assert np.all((out[0] & 0x7FFF) > 0x7F80)                       # NaN
+
+
+def test_rms_norm_power_of_two_scaling_invariance(oracle):
+    """With eps = 0, scaling a row by 2^k scales every partial sum by 4^k exactly, so
+    the output bits do not change. A missing square root or a wrong exponent breaks it."""
+    rng = np.random.default_rng(21)
+    x = _rand_bits(rng, (6, 2880), 1.0)
+    w = _rand_bits(rng, (2880,), 1.0)
+    base = oracle.rms_norm(x, w, 0.0)
+    for k in (3, -5, 17):
+        xs = x.astype(np.int32) + (k << 7)                           # exponent + k (no zeros/subnormals here)
+        assert np.all(np.abs(refmath.f32_of_bits(x)) > 2.0 ** -40)
+        got = oracle.rms_norm(xs.astype(np.uint16), w, 0.0)
+        assert np.array_equal(got, base), k
+
+
+@pytest.mark.parametrize("B,H,eps,sigma", [(4, 64, 1e-5, 1.0), (5, 2880, 1e-6, 3.0), (3, 300, 0.5, 0.3),
+                                           (2, 2888, 1e-5, 0.02)])
+def test_rms_norm_float64_bruteforce(oracle, B, H, eps, sigma):
+    """Within one bf16 step of x / sqrt(mean(x^2) + eps) * w evaluated in float64
+    (the fp32 sums and divisions are 2^-20 accurate; the last rounding is to bf16)."""
+    rng = np.random.default_rng(B * H)
+    x = _rand_bits(rng, (B, H), sigma)
+    w = _rand_bits(rng, (H,), 1.0)
+    got = oracle.rms_norm(x, w, eps)
+    ref = refmath.rms_norm_f64(x, w, eps)
+    ref_bits = refmath.bits_of_f32_rne(ref.astype(np.float32))
+    d = refmath.bf16_ulp_distance(got, ref_bits)
+    assert d.max() <= 1, (d.max(), np.argwhere(d > 1)[:4])
+    assert (d == 0).mean() > 0.99
+
+
+def test_rms_norm_follows_the_reference_summation_order(oracle):
+    """The 256 strided partials and the halving tree of rms_norm_gpu.hip:11-21 give a
+    different fp32 sum than a left-to-right sum on most long rows. A weight is chosen
+    so that the two sums round one output differently; the oracle must follow the tree."""
+    x, w, i, want_tree, want_serial = refmath.rms_order_sensitive_row(2880, seed=77)
+    out = oracle.rms_norm(x[None], w, 0.0)
+    assert out[0, i] == want_tree and want_tree != want_serial
+    # and the whole row equals the tree-order evaluation
+    v = refmath.f32_of_bits(x)
+    rms = np.sqrt(np.float32(refmath.sum_sq_f32(v, "tree") / np.float32(2880)))
+    assert np.array_equal(out[0], refmath.bits_of_f32_rne((v / rms) * refmath.f32_of_bits(w)))
+
+
+def test_residual_add_exact_rounding(oracle):
+    """bf16(a + b): the float64 sum of two bf16 values is exact, so rounding it to
+    fp32 and then to bf16 is what one fp32 add followed by the bf16 rounding gives."""
+    rng = np.random.default_rng(5)
+    a = _rand_bits(rng, (4097,), 1.0)
+    b = _rand_bits(rng, (4097,), 2.0 ** -6)
+    b[:100] = _rand_bits(rng, (100,), 1e4)[:]
+    got = oracle.residual_add(a, b)
+    exact = refmath.bf16_bits_to_f64(a) + refmath.bf16_bits_to_f64(b)
+    assert np.array_equal(got, refmath.bits_of_f32_rne(exact.astype(np.float32)))
+    # specials: inf + -inf = NaN, -0 + -0 = -0, 0 + -0 = +0, max + max overflows, 1 + 2^-8 ties to even
+    a = np.array([0x7F80, 0x8000, 0x0000, 0x7F7F, 0x3F80, 0x3F81], dtype=np.uint16)
+    b = np.array([0xFF80, 0x8000, 0x8000, 0x7F7F, 0x3B80, 0x3B80], dtype=np.uint16)
+    got = oracle.residual_add(a, b)
+    assert (got[0] & 0x7FFF) > 0x7F80
+    assert got[1:].tolist() == [0x8000, 0x0000, 0x7F80, 0x3F80, 0x3F82]
+
+
+def test_moe_block_composition_and_bruteforce(oracle):
+    """or_moe_block = residual_add(or_moe_layer(or_rms_norm(x)), x) bit for bit, and
+    the float64 block (x + layer(rms_norm(x))) within the layer's tolerance."""
+    layer = syn.make_layer(8, 256, 128, 3, seed=15)
+    x = syn.make_x(9, 256, seed=16)
+    rng = np.random.default_rng(17)
+    nw = _rand_bits(rng, (256,), 0.5)
+    eps = 1e-5
+    r = oracle.moe_block(layer, x, nw, eps)
+    h = oracle.rms_norm(x, nw, eps)
+    m = oracle.moe_layer(layer, h)
+    assert np.array_equal(r["out"], oracle.residual_add(m["out"], x))
+    assert np.array_equal(r["idx"], m["idx"]) and np.array_equal(r["wts"], m["wts"])
+    href = refmath.round_bf16_f64(refmath.rms_norm_f64(x, nw, eps))
+    hbits = refmath.bits_of_f32_rne(href.astype(np.float32))
+    lay, ridx, _ = refmath.moe_layer_f64(layer, hbits)
+    ref = lay + refmath.bf16_bits_to_f64(x)
+    assert np.array_equal(r["idx"], ridx)
+    assert refmath.rel_l2(refmath.bf16_bits_to_f64(r["out"]), ref) < 4e-3

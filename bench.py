@@ -201,6 +201,27 @@ def main():
         stage_ms[j] = evs[0].elapsed_time(evs[1]) / args.steps
     assert torch.equal(out, ref_out), "staged entry points disagree with the layer entry point"
 
+    # ---- the block around the layer (moe.rs:238-313): RMSNorm alone, then the fused
+    # block entry (norm + layer + residual add) K times each, same weight rotation
+    nw = torch.from_numpy(syn.bf16_from_f32(np.full(H, 1.0, np.float32)).view(np.int16)).cuda()
+    hbuf = torch.empty_like(xd)
+    out_blk = torch.empty_like(out)
+    ws_blk = torch.empty(dl0.block_workspace_bytes(B), dtype=torch.uint8, device="cuda")
+    block_calls = [
+        lambda i: (L.launch_rms_norm(xd.data_ptr(), nw.data_ptr(), hbuf.data_ptr(), B, H, 1e-5, s), check()),
+        lambda i: copies[i % n_copies].block_forward(xd, nw, 1e-5, out_blk, ws_blk, stream=s),
+    ]
+    block_ms = np.zeros(2)
+    for j, call in enumerate(block_calls):
+        call(0)
+        torch.cuda.synchronize()
+        evs[0].record(stream)
+        for i in range(args.steps):
+            call(i)
+        evs[1].record(stream)
+        torch.cuda.synchronize()
+        block_ms[j] = evs[0].elapsed_time(evs[1]) / args.steps
+
     # ---- roofline of the dominant kernel (gate_up) ---------------------------------------
     gu_expert_bytes = (2 * I * H // 2) + (2 * I * H // 32) + 2 * (2 * I)
     gate_up_ms = float(stage_ms[1])
@@ -258,6 +279,9 @@ def main():
                   "hbm_frac": round(layer_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                   "stage_ms": {"route": round(stage_ms[0], 5), "gate_up": round(stage_ms[1], 5),
                                "down": round(stage_ms[2], 5), "combine": round(stage_ms[3], 5)},
+                  "block_ms": {"rms_norm": round(block_ms[0], 5), "block_forward": round(block_ms[1], 5),
+                               "note": "physllm_moe_block_forward = rms_norm + layer + residual add "
+                                       "fused into the combine (eager, one call per step)"},
                   "wall_s_timed_region": round(wall, 4),
                   "launch": "hip graph replay" if args.graph else "eager C-ABI call per step",
                   "eager_ms_per_step": round(eager_ms, 5)},

@@ -86,5 +86,26 @@ def build_host_test(verbose: bool = True) -> str:
     return out
 
 
+def build_checkpoint_tools(verbose: bool = True) -> list:
+    """tests/cpp/checkpoint_tool (g++, the safetensors reader and GPT-OSS layer view on
+    the CPU) and tests/cpp/gpt_oss_block (hipcc, loads a layer and runs the block)."""
+    root = os.path.dirname(HERE)
+    cpp = os.path.join(root, "tests", "cpp")
+    tool = os.path.join(cpp, "checkpoint_tool")
+    blk = os.path.join(cpp, "gpt_oss_block")
+    cmds = [
+        ["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", os.path.join(cpp, "checkpoint_tool.cpp"), "-o", tool],
+        [hipcc(), "-O2", "-std=c++17", os.path.join(cpp, "gpt_oss_block.cpp"), "-o", blk,
+         "-L" + HERE, "-lphysllm_moe", "-Wl,-rpath," + HERE, "-Wl,-rpath,$ORIGIN/../../physllm_amd"],
+    ]
+    for cmd in cmds:
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    if verbose:
+        print(f"built {tool} and {blk}")
+    return [tool, blk]
+
+
 if __name__ == "__main__":
     build()

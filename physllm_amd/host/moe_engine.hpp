@@ -4,8 +4,8 @@
 // runs a host loop over the k experts with per-expert allocations and blocking
 // copies (moe.rs:249-299); here the routing, the expert GEMVs/GEMMs and the
 // combine stay on the device, in one call, with a workspace allocated once per
-// layer. The RMSNorm before (moe.rs:240-244) and the residual add after
-// (moe.rs:310-311) are outside this path.
+// layer. forward_moe_block adds the RMSNorm before (moe.rs:239-244) and the
+// residual add after (moe.rs:310-311) in the same single call.
 #pragma once
 
 #include "rocm_backend.hpp"
@@ -65,6 +65,27 @@ class MoELayer {
             workspace_.raw_ptr(), workspace_.numel(), dev.raw_stream());
         if (rc != PHYSLLM_MOE_OK)
             throw rocm_backend::BackendError(rc, std::string("physllm_moe_layer_forward: ") +
+                                                     physllm_moe_last_error_message());
+        dev.synchronise();
+    }
+
+    // The whole MoE sub-layer, moe.rs:238-313 (steps 8-12): residual [B, H] is
+    // updated in place to residual + moe(rms_norm(residual, ffn_norm, eps)).
+    void forward_moe_block(const GpuDevice& dev, DeviceTensor<bf16>& residual, const DeviceTensor<bf16>& ffn_norm,
+                           float eps, DeviceTensor<int32_t>* expert_indices = nullptr,
+                           DeviceTensor<float>* expert_weights = nullptr) {
+        const int batch = (int)residual.rows();
+        if ((int)residual.cols() != shape_.hidden_dim || (int)ffn_norm.numel() != shape_.hidden_dim)
+            throw rocm_backend::BackendError(PHYSLLM_MOE_EINVAL, "forward_moe_block: hidden size mismatch");
+        const size_t need = physllm_moe_block_workspace_bytes(&cfg_, batch);
+        if (need == 0 && batch > 0) rocm_backend::moe_check("physllm_moe_block_workspace_bytes");
+        if (workspace_.numel() < need) workspace_ = DeviceTensor<uint8_t>::alloc({need});
+        const int rc = physllm_moe_block_forward(
+            &cfg_, &ptrs_, residual.raw_ptr(), ffn_norm.raw_ptr(), eps, batch, residual.raw_ptr(),
+            expert_indices ? expert_indices->raw_ptr() : nullptr, expert_weights ? expert_weights->raw_ptr() : nullptr,
+            workspace_.raw_ptr(), workspace_.numel(), dev.raw_stream());
+        if (rc != PHYSLLM_MOE_OK)
+            throw rocm_backend::BackendError(rc, std::string("physllm_moe_block_forward: ") +
                                                      physllm_moe_last_error_message());
         dev.synchronise();
     }

@@ -1,7 +1,8 @@
 // C++ host layer over libphysllm_moe's C ABI, mirroring PhysLLM's Rust crate
 // crates/rocm-backend: GpuDevice (src/device.rs:24-133), DeviceTensor<T>
-// (src/tensor.rs:21-146), BackendError (src/lib.rs:35-47) and the MoE operator
-// wrappers (src/ops.rs:597-696) with the same names, size derivation and error
+// (src/tensor.rs:21-146), BackendError (src/lib.rs:35-47), the MoE operator
+// wrappers (src/ops.rs:597-696) and the RMSNorm / residual-add wrappers around the
+// MoE layer (src/ops.rs:366-384, :421-435) with the same names, size derivation and error
 // behaviour: each wrapper launches on the device's stream, then synchronises and
 // throws BackendError if the launch or the stream reported an error.
 //
@@ -86,6 +87,12 @@ class DeviceTensor {
         t.copy_from_host(data);
         return t;
     }
+    // numel elements straight from host memory (e.g. a file mapping), no staging copy.
+    static DeviceTensor from_host(const T* data, std::vector<size_t> shape) {
+        DeviceTensor t = alloc(std::move(shape));
+        if (t.numel_) hip_check(hipMemcpy(t.ptr_, data, t.numel_ * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy H2D");
+        return t;
+    }
     DeviceTensor() = default;
     DeviceTensor(DeviceTensor&& o) noexcept
         : ptr_(std::exchange(o.ptr_, nullptr)), shape_(std::move(o.shape_)), numel_(std::exchange(o.numel_, 0)) {}
@@ -126,6 +133,24 @@ class DeviceTensor {
     std::vector<size_t> shape_;
     size_t numel_ = 0;
 };
+
+// ---- ops.rs:366-384, :421-435 (the steps either side of the MoE layer) ---------
+
+// ops.rs:366-384: batch = input.rows(), hidden = input.cols().
+inline void rms_norm_gpu(const GpuDevice& dev, const DeviceTensor<bf16>& input, const DeviceTensor<bf16>& weight,
+                         DeviceTensor<bf16>& output, float eps) {
+    launch_rms_norm(input.raw_ptr(), weight.raw_ptr(), output.raw_ptr(), (int)input.rows(), (int)input.cols(), eps,
+                    dev.raw_stream());
+    moe_check("launch_rms_norm");
+    dev.synchronise();
+}
+
+// ops.rs:421-435: output += residual over output.numel() elements.
+inline void residual_add_gpu(const GpuDevice& dev, DeviceTensor<bf16>& output, const DeviceTensor<bf16>& residual) {
+    launch_residual_add(output.raw_ptr(), residual.raw_ptr(), (int)output.numel(), dev.raw_stream());
+    moe_check("launch_residual_add");
+    dev.synchronise();
+}
 
 // ---- ops.rs:597-696 -----------------------------------------------------------
 

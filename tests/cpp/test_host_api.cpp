@@ -1,6 +1,7 @@
 // GPU test of the C++ host layer (physllm_amd/host) against the CPU oracle.
-// Exercises the ops.rs-style wrappers (router, expert forward, combine, dequant),
-// the whole-layer MoELayer::forward_moe_layer, and BackendError on bad input.
+// Exercises the ops.rs-style wrappers (router, expert forward, combine, dequant,
+// rms_norm, residual add), the whole-layer MoELayer::forward_moe_layer, the block
+// MoELayer::forward_moe_block, and BackendError on bad input.
 // Prints one line per check and exits nonzero on the first failure.
 #include <cmath>
 #include <cstdio>
@@ -94,6 +95,26 @@ int main() {
         check(idx.copy_to_host() == eidx, "layer top-k indices bit-exact");
         const double err = rel_l2(out.copy_to_host(), eout);
         check(err < 1e-2, "layer output rel L2 < 1e-2", err);
+
+        // ---- the block: rms_norm -> layer -> residual add, in place (moe.rs:238-313) ----
+        auto nw = bf16_vec(H, 0.5f);
+        auto nwd = DeviceTensor<bf16>::from_slice(nw, {(size_t)H});
+        auto resid = DeviceTensor<bf16>::from_slice(x, {(size_t)B, (size_t)H});
+        layer.forward_moe_block(dev, resid, nwd, 1e-5f, &idx, &wts);
+        std::vector<bf16> bout((size_t)B * H);
+        or_moe_block(&oc, &ow, x.data(), nw.data(), 1e-5f, B, bout.data(), eidx.data(), ew.data(), 4);
+        check(idx.copy_to_host() == eidx, "block top-k indices bit-exact");
+        const double berr = rel_l2(resid.copy_to_host(), bout);
+        check(berr < 1e-2, "block output rel L2 < 1e-2", berr);
+        // the same through the separate wrappers (ops.rs:366-384, :421-435)
+        auto hn = DeviceTensor<bf16>::alloc({(size_t)B, (size_t)H});
+        rms_norm_gpu(dev, xd, nwd, hn, 1e-5f);
+        std::vector<bf16> ehn((size_t)B * H);
+        or_rms_norm(x.data(), nw.data(), ehn.data(), B, H, 1e-5f);
+        check(hn.copy_to_host() == ehn, "rms_norm_gpu bit-exact");
+        layer.forward_moe_layer(dev, hn, out);
+        residual_add_gpu(dev, out, xd);
+        check(out.copy_to_host() == resid.copy_to_host(), "block == rms_norm_gpu + layer + residual_add_gpu");
     }
 
     // ---- legacy wrappers (ops.rs:597-696) ----

@@ -223,3 +223,37 @@ def test_block_errors_on_device_path():
     dl.block_forward(x, nw, 1e-5, out, ws)
     torch.cuda.synchronize()
     assert capi.last_error()[0] == 0
+
+
+@pytest.mark.parametrize("E,H,I,K,B", [(32, 2880, 2880, 4, 1), (32, 2880, 2880, 4, 64), (4, 256, 128, 2, 512)])
+def test_layer_and_block_replay_in_hip_graph(oracle, E, H, I, K, B):
+    """Layer and block captured once in a HIP graph (no host syncs, no memset nodes),
+    replayed three times with eager work and synchronisation between replays; every
+    replay must equal the eager result."""
+    say(f"hip graph replay E={E} B={B}")
+    layer = syn.make_layer(E, H, I, K, seed=B + 5)
+    x = syn.make_x(B, H, seed=B + 6)
+    nw = bits(np.random.default_rng(B), (H,), 0.5)
+    dl = ops.DeviceMoELayer.from_host(layer)
+    xt, nwt = dev(x).view(B, H), dev(nw)
+    out_l, out_b = torch.empty_like(xt), torch.empty_like(xt)
+    ws_l = torch.empty(dl.workspace_bytes(B), dtype=torch.uint8, device="cuda")
+    ws_b = torch.empty(dl.block_workspace_bytes(B), dtype=torch.uint8, device="cuda")
+    dl.forward(xt, out_l, ws_l)
+    dl.block_forward(xt, nwt, 1e-5, out_b, ws_b)
+    torch.cuda.synchronize()
+    ref_l, ref_b = out_l.clone(), out_b.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        dl.forward(xt, out_l, ws_l)
+        dl.block_forward(xt, nwt, 1e-5, out_b, ws_b)
+    other = dev(syn.make_x(B, H, seed=B + 7)).view(B, H)
+    for rep in range(3):
+        out_l.fill_(0)
+        out_b.fill_(0)
+        dl.forward(other, torch.empty_like(other), ws_l)     # eager work on the same workspace
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_l, ref_l), f"layer replay {rep} differs"
+        assert torch.equal(out_b, ref_b), f"block replay {rep} differs"

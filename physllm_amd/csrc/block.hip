@@ -4,18 +4,12 @@
 // legacy launchers kernels/rms_norm_gpu.hip:36-45 and kernels/residual_add.hip:12-19
 // with bf16 data.
 //
-// RMSNorm keeps the reference's summation order exactly, so that its output is
-// bit-identical: thread j of a 256-thread workgroup accumulates v*v over
-// i = j, j + 256, ... with one fma per element (hipcc contracts `tsum += v * v`
-// under HIP's default fp-contract), and the 256 partials are added by the tree
-// s = 128, 64, ..., 1 (p[j] += p[j + s]). The first two tree levels cross waves
-// (through LDS); the last six run inside wave 0 with lane shuffles, which add the
-// same operands in the same order. rms = sqrtf(p[0] / H + eps) and
-// out = bf16((v / rms) * w) use correctly rounded fp32 division and square root
-// (HIP's default), with contraction off.
+// RMSNorm keeps the reference's summation order exactly (rmsnorm.h), so that its
+// output is bit-identical.
 #include "capi_internal.h"
 #include "common.h"
 #include "experts.h"
+#include "rmsnorm.h"
 
 namespace physllm {
 
@@ -27,58 +21,19 @@ constexpr int kNormThreads = 256;
 template <bool VEC>
 __global__ __launch_bounds__(kNormThreads) void k_rms_norm(const uint16_t* x, const uint16_t* __restrict__ wt,
                                                            uint16_t* out, int H, float eps) {
-#pragma clang fp contract(off)
     __shared__ float part[128];
     __shared__ float rms_s;
     const int j = threadIdx.x;
     const size_t base = (size_t)blockIdx.x * H;
     const uint16_t* xr = x + base;
-    float t = 0.f;
-    for (int i = j; i < H; i += kNormThreads) {
-        const float v = bf16_to_f32(xr[i]);
-        t = __builtin_fmaf(v, v, t);
-    }
-    // level s = 128: waves 2, 3 hand their partials to waves 0, 1
-    if (j >= 128) part[j - 128] = t;
-    __syncthreads();
-    if (j < 128) t = t + part[j];
-    __syncthreads();
-    // level s = 64: wave 1 hands its partials to wave 0
-    if (j >= 64 && j < 128) part[j - 64] = t;
-    __syncthreads();
-    if (j < 64) {
-        t = t + part[j];
-        // levels s = 32 .. 1 inside wave 0: lane l < s adds lane l + s
-#pragma unroll
-        for (int s = 32; s > 0; s >>= 1) {
-            const float o = __shfl_down(t, s, 64);
-            t = t + o;
-        }
-        if (j == 0) rms_s = __builtin_sqrtf(t / (float)H + eps);
-    }
-    __syncthreads();
-    const float rms = rms_s;
+    const float rms = rms_of_row(xr, H, eps, part, &rms_s);
     if (VEC) {
         const uint4* xv = (const uint4*)xr;
         const uint4* wv = (const uint4*)wt;
         uint4* ov = (uint4*)(out + base);
-        for (int c = j; c < (H >> 3); c += kNormThreads) {
-            const uint4 a = xv[c], w = wv[c];
-            const uint32_t* ap = (const uint32_t*)&a;
-            const uint32_t* wp = (const uint32_t*)&w;
-            uint4 r;
-            uint32_t* rp = (uint32_t*)&r;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float lo = (bf16_lo(ap[u]) / rms) * bf16_lo(wp[u]);
-                const float hi = (bf16_hi(ap[u]) / rms) * bf16_hi(wp[u]);
-                rp[u] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
-            }
-            ov[c] = r;
-        }
+        for (int c = j; c < (H >> 3); c += kNormThreads) ov[c] = rms_apply8(xv[c], wv[c], rms);
     } else {
-        for (int i = j; i < H; i += kNormThreads)
-            out[base + i] = (uint16_t)f32_to_bf16((bf16_to_f32(xr[i]) / rms) * bf16_to_f32(wt[i]));
+        for (int i = j; i < H; i += kNormThreads) out[base + i] = (uint16_t)rms_apply1(xr[i], wt[i], rms);
     }
 }
 

@@ -137,9 +137,16 @@ extern "C" size_t physllm_moe_workspace_bytes(const physllm_moe_config* cfg, int
 enum { kStageRoute = 1, kStageGateUp = 2, kStageDown = 4, kStageCombine = 8, kStageAll = 15 };
 
 // `residual` (nullable) is added to the combined output: out = bf16(out + residual).
+// `norm_w` (nullable, batch-1 route only): the route stage normalises `norm_x` into
+// x (RMSNorm with eps) before routing it, in the same launch.
+static bool route1_path(const physllm_moe_config& c, int batch) {
+    return batch == 1 && !use_gemm(c, batch) && c.num_experts <= 256;
+}
+
 static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* w, const void* x, int batch,
                       void* out, void* topk_idx, void* topk_w, void* workspace, size_t workspace_bytes,
-                      hipStream_t s, int stages, const void* residual = nullptr) {
+                      hipStream_t s, int stages, const void* residual = nullptr, const void* norm_w = nullptr,
+                      float eps = 0.f, const void* norm_x = nullptr) {
     int rc = validate(cfg, batch);
     if (rc) return rc;
     if (batch == 0) return ok();
@@ -158,10 +165,11 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
 
     if (stages & kStageRoute) {
         const bool gemm = use_gemm(c, batch);
-        if (batch == 1 && !gemm && c.num_experts <= 256) {
+        if (route1_path(c, batch)) {
             // one token: the whole route (and the bucketing of its k pairs) in one launch
-            rc = route1_launch(x, w->router_w, w->router_b, c.hidden, c.num_experts, c.top_k, idx, wts, ws.counts,
-                               ws.offsets, ws.perm, ws.pos, ws.slots, ws.n_slots, ws.passes, ws.n_passes, s);
+            rc = route1_launch(norm_w ? norm_x : x, w->router_w, w->router_b, c.hidden, c.num_experts, c.top_k, idx,
+                               wts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.slots, ws.n_slots, ws.passes,
+                               ws.n_passes, s, norm_w, eps, norm_w ? (void*)x : nullptr);
         } else {
             rc = router_launch(x, w->router_w, w->router_b, batch, c.hidden, c.num_experts, c.top_k, idx, wts, s);
             // prefill: the GEMM's token-tile prefix; decode: the GEMV's pass table
@@ -281,6 +289,9 @@ extern "C" int physllm_moe_block_forward(const physllm_moe_config* cfg, const ph
         return set_error(PHYSLLM_MOE_EINVAL, "layer: null weight pointer");
     const hipStream_t s = (hipStream_t)stream;
     void* h = (char*)workspace + lay;
+    // a single token's norm runs inside its route launch
+    if (route1_path(*cfg, batch) && cfg->hidden <= kRoute1NormMaxH)
+        return run_stages(cfg, w, h, batch, out, topk_idx, topk_w, workspace, lay, s, kStageAll, x, norm_w, eps, x);
     if ((rc = rms_norm_launch(x, norm_w, h, batch, cfg->hidden, eps, s))) return rc;
     return run_stages(cfg, w, h, batch, out, topk_idx, topk_w, workspace, lay, s, kStageAll, x);
 }

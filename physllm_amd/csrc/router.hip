@@ -18,6 +18,7 @@
 // dependent arg-max rounds) and one wave per token writes the selection and its
 // softmax.
 #include "common.h"
+#include "rmsnorm.h"
 #include "capi_internal.h"
 #include "experts.h"
 
@@ -279,24 +280,55 @@ __global__ __launch_bounds__(kRouterThreads) void k_router(const uint16_t* __res
 // ---------------------------------------------------------------------------
 constexpr int kRoute1Threads = 1024;
 
-template <int EPI>
+// LDS of k_route1 (bytes): logits [E] f64 | selected values [32] f64 | selected ids
+// [32] i32 | (NORM) norm partials [128] f32 + rms | the normalised row [H] bf16
+__host__ __device__ inline uint32_t route1_norm_off(int E) { return (uint32_t)E * 8u + 32u * 8u + 32u * 4u; }
+__host__ __device__ inline uint32_t route1_row_off(int E) { return (route1_norm_off(E) + 129u * 4u + 15u) & ~15u; }
+
+// NORM: the route of the block's token (crates/llm-core/src/moe.rs:239-259) with the
+// RMSNorm in front: h = bf16((x / rms) * norm_w) in the reference's order
+// (rmsnorm.h), written to h_out for the expert projections and kept in LDS as the
+// router's input, so the norm costs no launch of its own.
+template <int EPI, bool NORM>
 __global__ __launch_bounds__(kRoute1Threads) void k_route1(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias, int H, int E,
     int K, int32_t* __restrict__ idx, float* __restrict__ wts, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ pos, int4* __restrict__ slots,
-    int32_t* __restrict__ n_slots, int4* __restrict__ passes, int32_t* __restrict__ n_passes, int vec) {
-    extern __shared__ double lg[];  // [E] logits | selected values [32] | selected ids [32]
+    int32_t* __restrict__ n_slots, int4* __restrict__ passes, int32_t* __restrict__ n_passes, int vec,
+    const uint16_t* __restrict__ norm_w, float eps, uint16_t* __restrict__ h_out) {
+    extern __shared__ double lg[];  // layout: route1_norm_off / route1_row_off
     constexpr int NW = kRoute1Threads / 64;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint16_t* xin = x;
+    if (NORM) {
+        float* part = (float*)((char*)lg + route1_norm_off(E));
+        uint16_t* hrow = (uint16_t*)((char*)lg + route1_row_off(E));
+        const float rms = rms_of_row(x, H, eps, part, part + 128);
+        if (vec) {
+            for (int c = threadIdx.x; c < (H >> 3); c += kRoute1Threads) {
+                const uint4 hv = rms_apply8(((const uint4*)x)[c], ((const uint4*)norm_w)[c], rms);
+                ((uint4*)hrow)[c] = hv;
+                ((uint4*)h_out)[c] = hv;
+            }
+        } else {
+            for (int i = threadIdx.x; i < H; i += kRoute1Threads) {
+                const uint16_t hv = (uint16_t)rms_apply1(x[i], norm_w[i], rms);
+                hrow[i] = hv;
+                h_out[i] = hv;
+            }
+        }
+        __syncthreads();
+        xin = hrow;
+    }
     for (int e0 = wave * EPI; e0 < E; e0 += NW * EPI) {
         double acc[EPI][1];
         if (vec) {
-            router_dots<1, EPI, 6>(x, w, 0, 1, e0, E, H, lane, acc);
+            router_dots<1, EPI, 6>(xin, w, 0, 1, e0, E, H, lane, acc);
         } else {
 #pragma unroll
             for (int ei = 0; ei < EPI; ++ei) acc[ei][0] = 0.0;
             for (int d = lane; d < H; d += 64) {
-                const float xv = bf16_to_f32(x[d]);
+                const float xv = bf16_to_f32(xin[d]);
 #pragma unroll
                 for (int ei = 0; ei < EPI; ++ei)
                     if (e0 + ei < E) acc[ei][0] = acc_prod(acc[ei][0], xv, bf16_to_f32(w[(size_t)(e0 + ei) * H + d]));
@@ -354,14 +386,23 @@ __global__ __launch_bounds__(kRoute1Threads) void k_route1(
 
 int route1_launch(const void* x, const void* w, const void* bias, int H, int E, int K, void* idx, void* wts,
                   void* counts, void* offsets, void* perm, void* pos, void* slots, void* n_slots, void* passes,
-                  void* n_passes, hipStream_t stream) {
+                  void* n_passes, hipStream_t stream, const void* norm_w, float eps, void* h_out) {
     if (E > kRankMax || K > E || K > kMaxTopK) return set_error(PHYSLLM_MOE_EINVAL, "route1: sizes out of range");
-    const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0);
-    const size_t lds = (size_t)E * sizeof(double) + 32 * 8 + 32 * 4;
-    hipLaunchKernelGGL((k_route1<2>), dim3(1), dim3(kRoute1Threads), lds, stream, (const uint16_t*)x,
-                       (const uint16_t*)w, (const uint16_t*)bias, H, E, K, (int32_t*)idx, (float*)wts,
-                       (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm, (int32_t*)pos, (int4*)slots,
-                       (int32_t*)n_slots, (int4*)passes, (int32_t*)n_passes, vec);
+    if (norm_w && (!h_out || H > kRoute1NormMaxH)) return set_error(PHYSLLM_MOE_EINVAL, "route1: bad norm arguments");
+    const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0) &&
+                    (!norm_w || ((uintptr_t)norm_w % 16 == 0 && (uintptr_t)h_out % 16 == 0));
+    const size_t lds = norm_w ? (size_t)route1_row_off(E) + (size_t)H * 2 : (size_t)E * sizeof(double) + 32 * 8 + 32 * 4;
+    if (norm_w)
+        hipLaunchKernelGGL((k_route1<2, true>), dim3(1), dim3(kRoute1Threads), lds, stream, (const uint16_t*)x,
+                           (const uint16_t*)w, (const uint16_t*)bias, H, E, K, (int32_t*)idx, (float*)wts,
+                           (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm, (int32_t*)pos, (int4*)slots,
+                           (int32_t*)n_slots, (int4*)passes, (int32_t*)n_passes, vec, (const uint16_t*)norm_w, eps,
+                           (uint16_t*)h_out);
+    else
+        hipLaunchKernelGGL((k_route1<2, false>), dim3(1), dim3(kRoute1Threads), lds, stream, (const uint16_t*)x,
+                           (const uint16_t*)w, (const uint16_t*)bias, H, E, K, (int32_t*)idx, (float*)wts,
+                           (int32_t*)counts, (int32_t*)offsets, (int32_t*)perm, (int32_t*)pos, (int4*)slots,
+                           (int32_t*)n_slots, (int4*)passes, (int32_t*)n_passes, vec, nullptr, 0.f, nullptr);
     return check_launch("route1");
 }
 

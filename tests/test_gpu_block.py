@@ -185,10 +185,11 @@ def _separate_calls(dl, x, nw, eps):
 
 
 @pytest.mark.parametrize("E,H,I,K,B", [(4, 64, 64, 2, 3), (8, 256, 128, 3, 20), (32, 2880, 2880, 4, 1),
+                                       (8, 256, 128, 3, 1), (200, 96, 64, 5, 1),
                                        (32, 2880, 2880, 4, 64), (4, 256, 128, 2, 512), (128, 256, 128, 4, 2048)])
 def test_block_forward(oracle, E, H, I, K, B):
-    """Batch 1 (fused route), decode GEMV, grouped GEMM (512 tokens on 4 experts) and
-    the two-pass router (2048 tokens, 128 experts)."""
+    """Batch 1 (the norm runs inside the fused route launch), decode GEMV, grouped
+    GEMM (512 tokens on 4 experts) and the two-pass router (2048 tokens, 128 experts)."""
     say(f"block E={E} H={H} I={I} K={K} B={B}")
     layer = syn.make_layer(E, H, I, K, seed=E + B)
     x = syn.make_x(B, H, seed=B + 1)

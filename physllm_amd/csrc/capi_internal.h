@@ -18,8 +18,13 @@ int check_launch(const char* what);
 
 int dequant_launch(const void* packed, const void* scales, void* out, int64_t numel, int block_size,
                    hipStream_t stream);
+// lg_ws (nullable): B * E doubles of workspace; mid-size batches then take the
+// two-launch router (logits, then selection), which needs it.
 int router_launch(const void* x, const void* w, const void* bias, int B, int H, int E, int K, void* idx,
-                  void* wts, hipStream_t stream);
+                  void* wts, hipStream_t stream, void* lg_ws = nullptr);
+// Whether router_launch takes the two-launch form for (B, E) when given lg_ws and
+// 16-byte-aligned rows with H % 8 == 0, outside the two-pass range.
+bool router_two_launch(int B, int E);
 // Batch-1 route: router, top-k, softmax and bucketing in one launch (E <= 256); with
 // norm_w, the token is first RMS-normalised into h_out and routed from there.
 int route1_launch(const void* x, const void* w, const void* bias, int H, int E, int K, void* idx, void* wts,

@@ -50,6 +50,7 @@ struct Workspace {
     int32_t* n_passes;
     int32_t* perm;
     int32_t* pos;
+    double* lg;   // [B][E] router logits (two-launch router)
     uint16_t* h;
     float* y;     // [split][N][H]
     int split;
@@ -99,6 +100,7 @@ static Workspace carve(const physllm_moe_config& c, int B, char* base) {
     w.n_passes = (int32_t*)take(4);
     w.perm = (int32_t*)take(N * 4);
     w.pos = (int32_t*)take(N * 4);
+    w.lg = (double*)take(router_two_launch(B, c.num_experts) ? (size_t)B * E * 8 : 0);
     w.h = (uint16_t*)take(N * (size_t)c.intermediate * 2);
     w.split = down_split(c, B);
     w.y = (float*)take((size_t)w.split * N * (size_t)c.hidden * 4);
@@ -171,7 +173,8 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
                                wts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.slots, ws.n_slots, ws.passes,
                                ws.n_passes, s, norm_w, eps, norm_w ? (void*)x : nullptr);
         } else {
-            rc = router_launch(x, w->router_w, w->router_b, batch, c.hidden, c.num_experts, c.top_k, idx, wts, s);
+            rc = router_launch(x, w->router_w, w->router_b, batch, c.hidden, c.num_experts, c.top_k, idx, wts, s,
+                               ws.lg);
             // prefill: the GEMM's token-tile prefix; decode: the GEMV's pass table
             if (!rc)
                 rc = bucket_launch(idx, N, c.num_experts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.slots,

@@ -702,8 +702,71 @@ __global__ __launch_bounds__(kRmxThreads) void k_router_mx(const uint16_t* __res
 // logits [TB][E] (fp64), then the selections [TB][32] (fp64 values, int ids)
 static size_t router_smem_bytes(int TB, int E) { return (size_t)TB * E * sizeof(double) + (size_t)TB * 32 * 12; }
 
+// ---------------------------------------------------------------------------
+// Router for mid-size batches (B * E >= kRl2MinWork, outside the two-pass path) in
+// two launches, so that no workgroup streams every router row (k_router's
+// one-token groups each read all E rows: 737 KB per token at E = 128):
+//   k_router_logits: a workgroup computes the logits of 8 tokens x 16 experts
+//     exactly as k_router does (router_dots: fp32 products summed in fp64 in the
+//     same lane order, the same wave reduction, + bias) into a [B][E] fp64 buffer;
+//   k_router_select: one workgroup per token ranks its logits (ballot_select,
+//     or arg-max rounds for E > 256) and takes the softmax.
+// The logits are bit-identical to k_router's (a lane visits its chunks
+// c = lane, lane + 64, ... in the same order for any unroll), so are the
+// selection and the weights.
+// ---------------------------------------------------------------------------
+constexpr int kRlTok = 8;                           // tokens per logits workgroup
+constexpr int kRlExp = 2 * (kRouterThreads / 64);   // experts per logits workgroup (2 per wave)
+constexpr int64_t kRl2MinWork = 8192;               // B * E from which the two launches pay
+
+__global__ __launch_bounds__(kRouterThreads) void k_router_logits(const uint16_t* __restrict__ x,
+                                                                  const uint16_t* __restrict__ w,
+                                                                  const uint16_t* __restrict__ bias, int B, int H,
+                                                                  int E, double* __restrict__ lg) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t0 = blockIdx.x * kRlTok;
+    const int ntb = min(kRlTok, B - t0);
+    const int e0 = blockIdx.y * kRlExp + wave * 2;
+    if (e0 >= E) return;
+    double acc[2][kRlTok];
+    router_dots<kRlTok, 2, 2>(x, w, t0, ntb, e0, E, H, lane, acc);
+#pragma unroll
+    for (int ei = 0; ei < 2; ++ei) {
+        const int e = e0 + ei;
+        const double b = (bias && e < E) ? (double)bf16_to_f32(bias[e]) : 0.0;
+#pragma unroll
+        for (int tb = 0; tb < kRlTok; ++tb) {
+            const double sum = wave_sum_f64(acc[ei][tb]);
+            if (lane == 0 && e < E && tb < ntb) lg[(size_t)(t0 + tb) * E + e] = sum + b;
+        }
+    }
+}
+
+constexpr int kRsThreads = 256;
+
+__global__ __launch_bounds__(kRsThreads) void k_router_select(const double* __restrict__ lg, int E, int K,
+                                                              int32_t* __restrict__ idx, float* __restrict__ wts) {
+    extern __shared__ double ls[];  // [E] logits | selected values [32] | selected ids [32]
+    constexpr int NW = kRsThreads / 64;
+    const int t = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int e = threadIdx.x; e < E; e += kRsThreads) ls[e] = lg[(size_t)t * E + e];
+    __syncthreads();
+    if (E <= kRankMax) {
+        double* selv = ls + E;
+        int32_t* seli = (int32_t*)(selv + 32);
+        ballot_select(ls, E, K, wave, NW, lane, seli, selv);
+        __syncthreads();
+        if (wave == 0) softmax_selected(seli, selv, K, lane, idx + (size_t)t * K, wts + (size_t)t * K);
+    } else if (wave == 0) {
+        select_topk(ls, E, K, lane, idx + (size_t)t * K, wts + (size_t)t * K);
+    }
+}
+
+bool router_two_launch(int B, int E) { return B >= kRlTok * 2 && (int64_t)B * E >= kRl2MinWork; }
+
 int router_launch(const void* x, const void* w, const void* bias, int B, int H, int E, int K, void* idx,
-                  void* wts, hipStream_t stream) {
+                  void* wts, hipStream_t stream, void* lg_ws) {
     if (B < 0 || H < 1 || E < 1 || K < 1) return set_error(PHYSLLM_MOE_EINVAL, "router: bad sizes");
     if (E > kMaxExperts) return set_error(PHYSLLM_MOE_EINVAL, "router: num_experts > 1024");
     if (K > E || K > kMaxTopK) return set_error(PHYSLLM_MOE_EINVAL, "router: top_k > min(num_experts, 32)");
@@ -723,6 +786,13 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
         hipLaunchKernelGGL(k_router_mx, dim3((B + kRmxTok - 1) / kRmxTok), dim3(kRmxThreads), (size_t)Lr.total, stream,
                            (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, B, H, E, K, (int32_t*)idx,
                            (float*)wts);
+    } else if (lg_ws && vec && router_two_launch(B, E)) {
+        hipLaunchKernelGGL(k_router_logits, dim3((B + kRlTok - 1) / kRlTok, (E + kRlExp - 1) / kRlExp),
+                           dim3(kRouterThreads), 0, stream, (const uint16_t*)x, (const uint16_t*)w,
+                           (const uint16_t*)bias, B, H, E, (double*)lg_ws);
+        if (int rc = check_launch("router logits")) return rc;
+        hipLaunchKernelGGL(k_router_select, dim3(B), dim3(kRsThreads), (size_t)E * 8 + 32 * 12, stream,
+                           (const double*)lg_ws, E, K, (int32_t*)idx, (float*)wts);
     } else if (B > 1024) {
         // prefill: 4 tokens per group share every loaded router row
         constexpr int TB = 4;

@@ -344,6 +344,29 @@ def test_layer_batch1_route_ties_and_nan(oracle):
     assert np.array_equal(np.isnan(nw), np.isnan(r["wts"]))
 
 
+@pytest.mark.parametrize("E,H,K,B", [(128, 256, 4, 100), (128, 2880, 4, 256), (300, 96, 8, 40), (96, 224, 2, 100)])
+def test_layer_two_launch_router(oracle, E, H, K, B):
+    """Mid-size batches (B * E >= 8192 outside the two-pass range) route in two
+    launches (logits of 8 tokens x 16 experts per workgroup, then one selection
+    workgroup per token): indices bit-exact and weights as the oracle's, with
+    ties to the lower index, a NaN token, and more than 256 experts (arg-max rounds)."""
+    layer = syn.make_layer(E, H, 64, K, seed=E + B)
+    rw = layer.router_w.copy()
+    rw[[9, 2, 5]] = rw[2]
+    rb = syn.bf16_to_f32(layer.router_b).copy()
+    rb[[2, 5, 9]] = 20.0
+    layer.router_w, layer.router_b = rw, syn.bf16_from_f32(rb)
+    x = syn.make_x(B, H, seed=B)
+    x[3, 7] = 0x7FC0
+    got, gidx, gw, _ = _run_layer(layer, x)
+    eidx, ew = oracle.router(x, layer.router_w, layer.router_b, K)
+    assert np.array_equal(gidx, eidx)
+    fin = ~np.isnan(ew)
+    assert np.array_equal(np.isnan(gw), ~fin)
+    assert np.allclose(gw[fin], ew[fin], rtol=1e-6, atol=1e-7)
+    assert gidx[0, :min(3, K)].tolist() == [2, 5, 9][:min(3, K)]
+
+
 def test_layer_without_biases(oracle):
     layer = syn.make_layer(8, 128, 64, 2, seed=4, with_bias=False)
     x = syn.make_x(9, 128, seed=4)

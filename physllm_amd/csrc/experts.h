@@ -41,6 +41,11 @@ int gemv_launch(int mode, const GemvParams& p, int max_slots, int max_tokens, hi
 // out = bf16(out + res) (the residual add after the layer; res may equal out).
 int combine_launch(const float* y, int nsplit, size_t split_stride, const int32_t* pos, const float* wts,
                    uint16_t* out, const uint16_t* res, int B, int H, int K, hipStream_t stream);
+// Batch 1: down projection of the k slots and the weighted combine in one launch
+// (out = bf16(sum_j w_j * y_j) [+ res]); down1_ok says whether (K, Kdim) fit it.
+bool down1_ok(int K, int Kdim);
+int down1_launch(const GemvParams& p, const float* wts, const int32_t* pos, uint16_t* out, const uint16_t* res,
+                 int K, hipStream_t stream);
 // RMSNorm of B rows of H bf16 values (out may equal x) and the bf16 residual add.
 int rms_norm_launch(const void* x, const void* w, void* out, int B, int H, float eps, hipStream_t stream);
 int residual_add_launch(void* out, const void* res, int64_t n, hipStream_t stream);

@@ -649,6 +649,135 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ y, co
     ((uint2*)(out + (size_t)t * H))[d4] = o;
 }
 
+// ---------------------------------------------------------------------------
+// Batch 1: the down projection of all k selected experts and the weighted
+// combine in one launch. Workgroup b owns output rows 16 * kD1Rt * b ..; wave
+// w = s * kD1Rt + t computes the 16-row tile t of slot s exactly as k_mx_gemv
+// does (the same stripes, k-steps, four accumulators and their sum, + bias), and
+// the workgroup then combines its rows over the k slots in k order through LDS
+// (out = bf16(sum_j w_j * y_j), then + residual): the combine launch and the
+// round trip of y through HBM disappear. K <= kD1MaxK, K range <= 92 MX blocks.
+// ---------------------------------------------------------------------------
+constexpr int kD1Rt = 1;     // 16-row tiles per slot per workgroup
+constexpr int kD1MaxK = 4;   // slots (selected experts) the workgroup holds (8 waves at most)
+constexpr int kD1MaxNB = 92;
+
+__global__ __launch_bounds__(64 * kD1Rt * kD1MaxK) void k_mx_down1(GemvParams p, const float* __restrict__ wts,
+                                                                  const int32_t* __restrict__ pos,
+                                                                  uint16_t* out, const uint16_t* res, int K) {
+    extern __shared__ uint4 lds[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int m = lane & 15, g = lane >> 4;
+    const int s = wave / kD1Rt, t = wave - s * kD1Rt;
+    const int NB = p.Kdim >> 5;
+    const int cu = NB * 4, su = cu + 1;  // activation units per row, LDS row stride
+    uint8_t* scl = (uint8_t*)lds + wave * kGemvSclSlice;          // this wave's tile scales [16][NB]
+    uint4* xs = lds + (K * kD1Rt) * kGemvSclSlice / 16;          // activation rows [K][su]
+    float* ys = (float*)(xs + K * su);                           // y [K][16 * kD1Rt]
+    const int rb0 = blockIdx.x * 16 * kD1Rt;                     // first output row of the workgroup
+    const int r0 = rb0 + t * 16;                                 // this wave's tile
+    const int4 si = p.slots[s];                                  // {expert, 1, sorted position, 0}
+    const int e = si.x;
+    const uint32_t row_bytes = (uint32_t)(p.Kdim >> 1);
+    const uint32_t exp_w = (uint32_t)p.R * row_bytes;
+    const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;
+    // activation row of slot s (h at sorted position si.z): the wave's lanes stage it
+    const __amdgpu_buffer_rsrc_t ract = make_rsrc(p.act + (size_t)si.z * p.Kdim, (uint32_t)p.Kdim * 2u);
+    u32x4_t xv[6];
+#pragma unroll
+    for (int u = 0; u < 6; ++u) xv[u] = buf_load16(ract, (uint32_t)(lane + 64 * u) * 16u, 0);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales + (size_t)e * exp_s, exp_s);
+    const uint32_t soff = (uint32_t)r0 * NB + lane * 16u;
+    const u32x4_t sv0 = buf_load16(rs, soff, 0);
+    const u32x4_t sv1 = buf_load16(rs, soff, 1024);
+    __builtin_amdgcn_sched_barrier(0);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.blocks + (size_t)e * exp_w, exp_w);
+    const uint32_t woff = (uint32_t)(r0 + m) * row_bytes + (uint32_t)g * 16u;
+    u32x4_t wq[kGemvNit];
+#pragma unroll
+    for (int j = 0; j < kGemvNit; ++j) wq[j] = buf_load16(rw, 4 * j < NB ? woff : kRsrcPast, 64 * j);
+    __builtin_amdgcn_sched_barrier(0);
+    ((u32x4_t*)scl)[lane] = sv0;
+    ((u32x4_t*)scl)[lane + 64] = sv1;
+    if (t == 0) {
+#pragma unroll
+        for (int u = 0; u < 6; ++u)
+            if (lane + 64 * u < cu) ((u32x4_t*)xs)[s * su + lane + 64 * u] = xv[u];
+    }
+    __syncthreads();
+    // k_mx_gemv's pass for one token (every B column reads the token's row)
+    const uint4* xl = xs + s * su + 4 * g;
+    const uint8_t* sl = scl + m * NB + g;
+    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+#pragma unroll
+    for (int j = 0; j < kGemvNit; ++j) {
+        if (4 * j < NB) {
+            const bool edge = 4 * j + 3 >= NB;
+            const bool bv = 4 * j + g < NB;
+            uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
+            asm volatile("" : "+v"(sj));
+            const float sf = e8m0_scale_operand(sj);
+            u32x4_t q = wq[j];
+            uint4 x0 = xl[16 * j + 0], x1 = xl[16 * j + 1], x2 = xl[16 * j + 2], x3 = xl[16 * j + 3];
+            if (edge && !bv) {
+                q = u32x4_t{0u, 0u, 0u, 0u};
+                x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
+            }
+            acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
+            acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
+            acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
+            acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
+        }
+    }
+    // column 0 holds the token: y of rows r0 + 4g .. + 3 (+ bias), into LDS
+    if (m == 0) {
+        const f32x4_t acc = (acc0 + acc1) + (acc2 + acc3);
+        const int rr = r0 + 4 * g;
+        float bsum[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias && rr < p.R) {
+            const uint2 bb = *(const uint2*)(p.bias + (size_t)e * p.R + rr);
+            bsum[0] = bf16_lo(bb.x);
+            bsum[1] = bf16_hi(bb.x);
+            bsum[2] = bf16_lo(bb.y);
+            bsum[3] = bf16_hi(bb.y);
+        }
+        float* yr = ys + s * (16 * kD1Rt) + t * 16 + 4 * g;
+        yr[0] = acc[0] + bsum[0];
+        yr[1] = acc[1] + bsum[1];
+        yr[2] = acc[2] + bsum[2];
+        yr[3] = acc[3] + bsum[3];
+    }
+    __syncthreads();
+    // combine (k_combine's order: fmaf over the k pairs in k order, one rounding)
+    const int i = threadIdx.x;
+    const int r = rb0 + i;
+    if (i < 16 * kD1Rt && r < p.R) {
+        float a = 0.f;
+        for (int j = 0; j < K; ++j) a = __builtin_fmaf(wts[j], ys[pos[j] * (16 * kD1Rt) + i], a);
+        uint32_t o = f32_to_bf16(a);
+        if (res) o = f32_to_bf16(bf16_to_f32(o) + bf16_to_f32(res[r]));
+        out[r] = (uint16_t)o;
+    }
+}
+
+bool down1_ok(int K, int Kdim) { return K >= 1 && K <= kD1MaxK && (Kdim >> 5) <= kD1MaxNB; }
+
+int down1_launch(const GemvParams& p, const float* wts, const int32_t* pos, uint16_t* out, const uint16_t* res,
+                 int K, hipStream_t stream) {
+    if (!down1_ok(K, p.Kdim)) return set_error(PHYSLLM_MOE_EINVAL, "down1: sizes out of range");
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void*)k_mx_down1, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr_set = true;
+    }
+    const int NB = p.Kdim >> 5;
+    const size_t lds = (size_t)K * kD1Rt * kGemvSclSlice + (size_t)K * (4 * NB + 1) * 16 +
+                       (size_t)K * 16 * kD1Rt * sizeof(float);
+    const unsigned grid = (unsigned)((p.R + 16 * kD1Rt - 1) / (16 * kD1Rt));
+    hipLaunchKernelGGL(k_mx_down1, dim3(grid), dim3(64 * kD1Rt * K), lds, stream, p, wts, pos, out, res, K);
+    return check_launch("down1");
+}
+
 int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, hipStream_t stream) {
     GemvParams p = p0;
     if (p.split < 1 || p.split > kMaxSplit) return set_error(PHYSLLM_MOE_EINVAL, "gemv: bad split");

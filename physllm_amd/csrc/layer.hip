@@ -212,6 +212,9 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
                                 : gemv_launch(kModeGateUp, p, max_slots, batch, s);
         if (rc) return rc;
     }
+    // one token: the down projection and the combine run as one launch
+    const bool down1 = batch == 1 && (stages & kStageDown) && (stages & kStageCombine) && !use_gemm(c, batch) &&
+                       down1_ok(c.top_k, c.intermediate);
     if (stages & kStageDown) {
         p.act = ws.h;
         p.act_rows = N;
@@ -222,11 +225,16 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
         p.Kdim = c.intermediate;
         p.R = c.hidden;
         p.split = ws.split;
-        rc = use_gemm(c, batch) ? gemm_launch(kModeDown, p, ws.tprefix, max_slots, N, s)
-                                : gemv_launch(kModeDown, p, max_slots, batch, s);
+        if (down1) {
+            p.split = 1;
+            rc = down1_launch(p, wts, ws.pos, (uint16_t*)out, (const uint16_t*)residual, c.top_k, s);
+        } else {
+            rc = use_gemm(c, batch) ? gemm_launch(kModeDown, p, ws.tprefix, max_slots, N, s)
+                                    : gemv_launch(kModeDown, p, max_slots, batch, s);
+        }
         if (rc) return rc;
     }
-    if (stages & kStageCombine) {
+    if ((stages & kStageCombine) && !down1) {
         if ((rc = combine_launch(ws.y, ws.split, (size_t)N * c.hidden, ws.pos, wts, (uint16_t*)out,
                                  (const uint16_t*)residual, batch, c.hidden, c.top_k, s)))
             return rc;

@@ -170,6 +170,19 @@ def main():
     if graphs:
         assert torch.equal(out, ref_out), "timed replays changed the output"
 
+    # ---- per-step spread: K more steps, each between its own pair of events (after the
+    # timed region, so the reported value is not affected); median and 10/90th percentiles
+    pev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    pev[0].record(stream)
+    for i in range(args.steps):
+        if graphs:
+            graphs[i % n_copies].replay()
+        else:
+            step(i)
+        pev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per_step = np.array([pev[i].elapsed_time(pev[i + 1]) for i in range(args.steps)])
+
     # ---- per-stage timing: each stage entry point launched K times back to back
     # (rotating weight copies) between two events on the launch stream; the stages
     # are idempotent given the routing state the route stage left in the workspace.
@@ -282,6 +295,10 @@ def main():
                   "block_ms": {"rms_norm": round(block_ms[0], 5), "block_forward": round(block_ms[1], 5),
                                "note": "physllm_moe_block_forward = rms_norm + layer + residual add "
                                        "fused into the combine (eager, one call per step)"},
+                  "per_step_ms": {"median": round(float(np.median(per_step)), 5),
+                                  "p10": round(float(np.percentile(per_step, 10)), 5),
+                                  "p90": round(float(np.percentile(per_step, 90)), 5),
+                                  "steps": int(args.steps)},
                   "wall_s_timed_region": round(wall, 4),
                   "launch": "hip graph replay" if args.graph else "eager C-ABI call per step",
                   "eager_ms_per_step": round(eager_ms, 5)},
@@ -322,6 +339,14 @@ def bench_dequant(args):
     wall = time.perf_counter() - t0
     ms = ev0.elapsed_time(ev1) / args.steps
     gbs = alg / (ms * 1e-3) / 1e9
+    # per-launch spread (after the timed region): median and 10/90th percentiles
+    pev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    pev[0].record(stream)
+    for i in range(args.steps):
+        ops.mxfp4_dequant(pd, sd, out, s)
+        pev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per_step = np.array([pev[i].elapsed_time(pev[i + 1]) for i in range(args.steps)])
 
     # spot check: one expert's slab against the oracle (bit-exact)
     from oracle import oracle as orc
@@ -366,7 +391,11 @@ def bench_dequant(args):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(1, "dequant"),
                      "kernel": "k_mxfp4_dequant32", "work_per_launch": alg},
-        "layer": {"wall_s_timed_region": round(wall, 4), "launch": "eager C-ABI call per step"},
+        "layer": {"wall_s_timed_region": round(wall, 4), "launch": "eager C-ABI call per step",
+                  "per_step_ms": {"median": round(float(np.median(per_step)), 5),
+                                  "p10": round(float(np.percentile(per_step, 10)), 5),
+                                  "p90": round(float(np.percentile(per_step, 90)), 5),
+                                  "steps": int(args.steps)}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)

@@ -26,7 +26,8 @@
  *   or_bucket : permutation invariants + numpy stable argsort.
  *   or_swiglu : closed-form points (clamp corners, NaN propagation).
  *   or_moe_layer / or_moe_experts : float64 numpy brute force on tiny shapes
- *       using weights decoded by an independent decoder; committed golden fixture.
+ *       using weights decoded by an independent decoder; the committed fixture
+ *       tests/golden/tiny_layer.npz freezes that brute force for one seeded layer.
  *   or_legacy_* : float64 numpy brute force.
  *   or_rms_norm : closed forms (constant rows, a single nonzero element, power-of-two
  *       scaling of a row with eps = 0 leaves it unchanged), the float64 brute force

@@ -372,3 +372,34 @@ def test_moe_block_composition_and_bruteforce(oracle):
     ref = lay + refmath.bf16_bits_to_f64(x)
     assert np.array_equal(r["idx"], ridx)
     assert refmath.rel_l2(refmath.bf16_bits_to_f64(r["out"]), ref) < 4e-3
+
+
+# ---- committed fixtures (tests/golden/make_fixtures.py) ------------------------------
+
+def _golden(name):
+    import os
+    return os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)
+
+
+def test_golden_mxfp4_kat_fixture(oracle):
+    """The frozen exact-rational table: the oracle's value for every (scale, code)."""
+    kat = np.load(_golden("mxfp4_kat.npy"))
+    assert kat.shape == (256, 16) and kat.dtype == np.uint16
+    got = np.array([[oracle.mxfp4_value_bf16(c, s) for c in range(16)] for s in range(256)], dtype=np.uint16)
+    assert np.array_equal(got, kat)
+    assert np.array_equal(refmath.mxfp4_kat(), kat)
+
+
+def test_golden_tiny_layer_fixture(oracle):
+    """The frozen float64 brute force of a seeded 4-expert layer: same top-k, same
+    routing weights, outputs within the bf16 rounding of the layer."""
+    d = np.load(_golden("tiny_layer.npz"))
+    E, H, I, K = (int(v) for v in d["shape"])
+    layer = syn.MoELayer(H, I, E, K, d["router_w"], d["router_b"], d["gate_up_blocks"], d["gate_up_scales"],
+                         d["gate_up_bias"], d["down_blocks"], d["down_scales"], d["down_bias"])
+    r = oracle.moe_layer(layer, d["x"])
+    assert np.array_equal(r["idx"], d["idx"])
+    assert np.allclose(r["wts"], d["w"], rtol=1e-6)
+    got = refmath.bf16_bits_to_f64(r["out"])
+    assert refmath.rel_l2(got, d["out_f64"]) < 4e-3
+    assert np.max(np.abs(got - d["out_f64"])) <= 8 * 2.0 ** -8 * np.max(np.abs(d["out_f64"]))

@@ -344,17 +344,20 @@ def test_layer_batch1_route_ties_and_nan(oracle):
     assert np.array_equal(np.isnan(nw), np.isnan(r["wts"]))
 
 
-@pytest.mark.parametrize("E,H,K,B", [(128, 256, 4, 100), (128, 2880, 4, 256), (300, 96, 8, 40), (96, 224, 2, 100)])
+@pytest.mark.parametrize("E,H,K,B", [(128, 256, 4, 100), (128, 2880, 4, 256), (300, 96, 8, 40), (96, 224, 2, 100),
+                                     (64, 256, 4, 100), (32, 2880, 4, 64), (40, 96, 1, 17), (8, 128, 8, 127)])
 def test_layer_two_launch_router(oracle, E, H, K, B):
     """Mid-size batches (B * E >= 8192 outside the two-pass range) route in two
     launches (logits of 8 tokens x 16 experts per workgroup, then one selection
-    workgroup per token): indices bit-exact and weights as the oracle's, with
-    ties to the lower index, a NaN token, and more than 256 experts (arg-max rounds)."""
+    workgroup per token); the smaller ones here take k_router. Indices bit-exact and
+    weights as the oracle's, with ties to the lower index, a NaN token, more than 256
+    experts (arg-max rounds), k = 1 and k = E."""
     layer = syn.make_layer(E, H, 64, K, seed=E + B)
+    tie = [2, 5, 9] if E > 9 else [1, 3, 5]
     rw = layer.router_w.copy()
-    rw[[9, 2, 5]] = rw[2]
+    rw[tie] = rw[tie[0]]
     rb = syn.bf16_to_f32(layer.router_b).copy()
-    rb[[2, 5, 9]] = 20.0
+    rb[tie] = 20.0
     layer.router_w, layer.router_b = rw, syn.bf16_from_f32(rb)
     x = syn.make_x(B, H, seed=B)
     x[3, 7] = 0x7FC0
@@ -364,7 +367,7 @@ def test_layer_two_launch_router(oracle, E, H, K, B):
     fin = ~np.isnan(ew)
     assert np.array_equal(np.isnan(gw), ~fin)
     assert np.allclose(gw[fin], ew[fin], rtol=1e-6, atol=1e-7)
-    assert gidx[0, :min(3, K)].tolist() == [2, 5, 9][:min(3, K)]
+    assert gidx[0, :min(3, K)].tolist() == tie[:min(3, K)]
 
 
 def test_layer_without_biases(oracle):

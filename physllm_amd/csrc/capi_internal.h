@@ -25,6 +25,9 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
 // Whether router_launch takes the two-launch form for (B, E) when given lg_ws and
 // 16-byte-aligned rows with H % 8 == 0, outside the two-pass range.
 bool router_two_launch(int B, int E);
+// Whether the layer's router takes the tiled two-pass form (bounds, then selection) for
+// (B, E), which needs lg_ws as well (B * E float2 bounds).
+bool rmx_tiled(int B, int E);
 // Batch-1 route: router, top-k, softmax and bucketing in one launch (E <= 256); with
 // norm_w, the token is first RMS-normalised into h_out and routed from there.
 int route1_launch(const void* x, const void* w, const void* bias, int H, int E, int K, void* idx, void* wts,

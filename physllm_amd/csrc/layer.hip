@@ -104,7 +104,10 @@ static Workspace carve(const physllm_moe_config& c, int B, char* base) {
     w.n_passes = (int32_t*)take(4);
     w.perm = (int32_t*)take(N * 4);
     w.pos = (int32_t*)take(N * 4);
-    w.lg = (double*)take(router_two_launch(B, c.num_experts) ? (size_t)B * E * 8 : 0);
+    // router logits (two-launch router) or bounds (tiled two-pass router), B x E x 8
+    // bytes; null when neither router form can run, so no router writes an empty region
+    const bool need_lg = router_two_launch(B, c.num_experts) || rmx_tiled(B, c.num_experts);
+    w.lg = need_lg ? (double*)take((size_t)B * E * 8) : nullptr;
     w.h = (uint16_t*)take(N * (size_t)c.intermediate * 2);
     w.split = down_split(c, B);
     w.y = (float*)take((size_t)w.split * N * (size_t)c.hidden * 4);

@@ -765,6 +765,207 @@ __global__ __launch_bounds__(kRsThreads) void k_router_select(const double* __re
 
 bool router_two_launch(int B, int E) { return B >= kRlTok * 2 && (int64_t)B * E >= kRl2MinWork; }
 
+bool rmx_tiled(int B, int E) { return B >= kRmxMinBatch && E > 64 && E <= kRmxMaxE; }
+
+// ---------------------------------------------------------------------------
+// Tiled two-pass router (inside the layer, where the workspace holds the bounds):
+// the same bounds, candidate rule and exact arithmetic as k_router_mx, in two
+// launches so that no workgroup streams every router row or computes every
+// candidate of 16 tokens alone.
+//   k_rmx_bounds: workgroup (16 tokens, 16 experts); its 8 waves split K and load
+//     their weight and activation fragments straight from memory (no staging),
+//     wave 0 adds the parts in order and writes each (token, expert)'s [lo, hi] to
+//     a [B][E] buffer, or (-inf, +inf) where an approximate sum is not finite;
+//   k_rmx_select: one wave per token: threshold T (k-th largest lo), candidates
+//     hi >= T (every expert when any bound is (-inf, +inf)), their exact logits
+//     (fp32 products summed in fp64 in k_router's lane order, + bias), the
+//     selection among them (ballot_select) and the softmax.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kRmxThreads) void k_rmx_bounds(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ bias, int B, int H, int E,
+                                                            float2* __restrict__ lohi) {
+    __shared__ float red[kRmxWaves][8][64];
+    __shared__ float wxs[kRmxWaves][32];
+    const int t0 = blockIdx.x * kRmxTok;
+    const int ntok = min(kRmxTok, B - t0);
+    const int tile = blockIdx.y;  // experts 16 * tile ..
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int m = lane & 15, g = lane >> 4;
+    const int nc = H >> 5;
+    const int cb = wave * nc / kRmxWaves, ce = (wave + 1) * nc / kRmxWaves;
+    {
+        const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)E * (uint32_t)H * 2u);
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)t0 * H, (uint32_t)ntok * (uint32_t)H * 2u);
+        const uint32_t wrow = (uint32_t)(tile * 16 + m) * (uint32_t)H * 2u + (uint32_t)g * 16u;
+        const uint32_t xrow = (uint32_t)m * (uint32_t)H * 2u + (uint32_t)g * 16u;
+        const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, accS = acc, accW = acc, accX = acc;
+        constexpr int D = 6;  // chunks in flight per wave
+        u32x4_t wb[D], xb[D];
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            wb[i] = buf_load16(rw, cb + i < ce ? wrow + (uint32_t)(cb + i) * 64u : kRsrcPast, 0);
+            xb[i] = buf_load16(rx, cb + i < ce ? xrow + (uint32_t)(cb + i) * 64u : kRsrcPast, 0);
+        }
+        for (int c0 = cb; c0 < ce; c0 += D) {
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                const int c = c0 + i;
+                if (c < ce) {  // wave-uniform
+                    const u32x4_t q = wb[i], r = xb[i];
+                    const uint4 wv = make_uint4(q[0], q[1], q[2], q[3]);
+                    const uint4 xv = make_uint4(r[0], r[1], r[2], r[3]);
+                    const uint4 wa = bf16x8_abs(wv), xa = bf16x8_abs(xv);
+                    acc = mfma16x16x32(as_bf16x8(wv), as_bf16x8(xv), acc);
+                    accS = mfma16x16x32(as_bf16x8(wa), as_bf16x8(xa), accS);
+                    accW = mfma16x16x32(as_bf16x8(wa), as_bf16x8(ones), accW);
+                    accX = mfma16x16x32(as_bf16x8(ones), as_bf16x8(xa), accX);
+                }
+                wb[i] = buf_load16(rw, c + D < ce ? wrow + (uint32_t)(c + D) * 64u : kRsrcPast, 0);
+                xb[i] = buf_load16(rx, c + D < ce ? xrow + (uint32_t)(c + D) * 64u : kRsrcPast, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            red[wave][i][lane] = acc[i];
+            red[wave][4 + i][lane] = accS[i];
+        }
+        if (m == 0)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wxs[wave][4 * g + i] = accW[i];
+        if (g == 0) wxs[wave][16 + m] = accX[0];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const float u = 0x1p-23f;
+    const double mr = 33.0 * nc + 16.0;
+    const double gm = mr * (double)u / (1.0 - mr * (double)u);
+    const double cab = (33.0 * nc + H + 16.0) * 0x1p-125;
+    float a[4] = {0.f, 0.f, 0.f, 0.f}, S[4] = {0.f, 0.f, 0.f, 0.f}, W1[4] = {0.f, 0.f, 0.f, 0.f}, X1 = 0.f;
+    for (int p2 = 0; p2 < kRmxWaves; ++p2) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] += red[p2][i][lane];
+            S[i] += red[p2][4 + i][lane];
+            W1[i] += wxs[p2][4 * g + i];
+        }
+        X1 += wxs[p2][16 + m];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = tile * 16 + 4 * g + i;
+        if (e < E && m < ntok) {
+            const float bb = bias ? bf16_to_f32(bias[e]) : 0.f;
+            const float ab = a[i] + bb;
+            const double eps = gm / (1.0 - gm) * ((double)S[i] + cab) + cab +
+                               0x1p-126 * ((double)W1[i] + (double)X1) * (1.0 + 2.0 * gm) +
+                               (double)u * fabs((double)ab);
+            const bool fin = __builtin_isfinite(ab) && __builtin_isfinite(S[i]) && __builtin_isfinite(W1[i]) &&
+                             __builtin_isfinite(X1) && __builtin_isfinite(eps);
+            const double e2 = eps * (1.0 + 0x1p-20);
+            lohi[(size_t)(t0 + m) * E + e] =
+                fin ? make_float2(__double2float_rd((double)ab - e2), __double2float_ru((double)ab + e2))
+                    : make_float2(-INFINITY, INFINITY);
+        }
+    }
+}
+
+constexpr int kRsWaves = 2;  // tokens (one per wave) per selection workgroup: spread over the CUs
+
+__global__ __launch_bounds__(64 * kRsWaves) void k_rmx_select(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ bias, int B, int H, int E,
+                                                            int K, const float2* __restrict__ lohi,
+                                                            int32_t* __restrict__ idx, float* __restrict__ wts) {
+    __shared__ double exact[kRsWaves][kRmxMaxE];
+    __shared__ int32_t cand[kRsWaves][kRmxMaxE];
+    __shared__ double selv[kRsWaves][32];
+    __shared__ int32_t seli[kRsWaves][32];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = blockIdx.x * kRsWaves + wave;
+    if (t >= B) return;  // no workgroup barriers below
+    const float2* lh = lohi + (size_t)t * E;
+    const bool v0 = lane < E, v1 = lane + 64 < E;
+    const float2 q0 = v0 ? lh[lane] : make_float2(0.f, 0.f);
+    const float2 q1 = v1 ? lh[lane + 64] : make_float2(0.f, 0.f);
+    const bool all = __ballot((v0 && q0.x == -INFINITY && q0.y == INFINITY) ||
+                              (v1 && q1.x == -INFINITY && q1.y == INFINITY)) != 0ull;
+    bool c0 = v0, c1 = v1;
+    if (!all) {
+        // T = k-th largest lower bound: k rounds, each removing one largest
+        float l0 = v0 ? q0.x : -INFINITY, l1 = v1 ? q1.x : -INFINITY;
+        bool r0 = !v0, r1 = !v1;
+        float T = -INFINITY;
+        for (int j = 0; j < K; ++j) {
+            float mx = fmaxf(r0 ? -INFINITY : l0, r1 ? -INFINITY : l1);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            T = mx;
+            const uint64_t b0 = __ballot(!r0 && l0 == mx), b1 = __ballot(!r1 && l1 == mx);
+            if (b0) {
+                if (lane == __builtin_ctzll(b0)) r0 = true;
+            } else if (b1) {
+                if (lane == __builtin_ctzll(b1)) r1 = true;
+            }
+        }
+        c0 = v0 && q0.y >= T;
+        c1 = v1 && q1.y >= T;
+    }
+    const uint64_t m0 = __ballot(c0), m1 = __ballot(c1);
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int n0 = __popcll(m0);
+    const int nc = n0 + __popcll(m1);
+    if (c0) cand[wave][__popcll(m0 & lt)] = lane;
+    if (c1) cand[wave][n0 + __popcll(m1 & lt)] = lane + 64;
+    __builtin_amdgcn_wave_barrier();
+    // exact logits of the candidates, two at a time (k_router's lane order)
+    const int nch = H >> 3;
+    const uint4* xr = (const uint4*)(x + (size_t)t * H);
+    uint4 xv[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const int c = lane + 64 * i;
+        xv[i] = c < nch ? xr[c] : make_uint4(0, 0, 0, 0);
+    }
+    for (int j = 0; j < nc; j += 2) {
+        const bool hb = j + 1 < nc;
+        const int ea = cand[wave][j], eb = cand[wave][hb ? j + 1 : j];
+        const uint4* wa = (const uint4*)(w + (size_t)ea * H);
+        const uint4* wbp = (const uint4*)(w + (size_t)eb * H);
+        uint4 qa[6], qb[6];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            const int c = lane + 64 * i;
+            qa[i] = c < nch ? wa[c] : make_uint4(0, 0, 0, 0);
+            qb[i] = c < nch ? wbp[c] : make_uint4(0, 0, 0, 0);
+        }
+        double sa = 0.0, sb = 0.0;
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            float xf[8], wf[8];
+            bf16x8_to_f32(xv[i], xf);
+            bf16x8_to_f32(qa[i], wf);
+#pragma unroll
+            for (int k2 = 0; k2 < 8; ++k2) sa = acc_prod(sa, xf[k2], wf[k2]);
+            bf16x8_to_f32(qb[i], wf);
+#pragma unroll
+            for (int k2 = 0; k2 < 8; ++k2) sb = acc_prod(sb, xf[k2], wf[k2]);
+        }
+        const double ra = wave_sum_f64(sa), rb = wave_sum_f64(sb);
+        if (lane == 0) {
+            exact[wave][j] = ra + (bias ? (double)bf16_to_f32(bias[ea]) : 0.0);
+            if (hb) exact[wave][j + 1] = rb + (bias ? (double)bf16_to_f32(bias[eb]) : 0.0);
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    ballot_select(exact[wave], nc, K, 0, 1, lane, seli[wave], selv[wave]);
+    __builtin_amdgcn_wave_barrier();
+    if (lane < K) seli[wave][lane] = cand[wave][seli[wave][lane]];
+    __builtin_amdgcn_wave_barrier();
+    softmax_selected(seli[wave], selv[wave], K, lane, idx + (size_t)t * K, wts + (size_t)t * K);
+}
+
 int router_launch(const void* x, const void* w, const void* bias, int B, int H, int E, int K, void* idx,
                   void* wts, hipStream_t stream, void* lg_ws) {
     if (B < 0 || H < 1 || E < 1 || K < 1) return set_error(PHYSLLM_MOE_EINVAL, "router: bad sizes");
@@ -773,7 +974,18 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
     if (B == 0) return ok();
     if (!x || !w || !idx || !wts) return set_error(PHYSLLM_MOE_EINVAL, "router: null pointer");
     const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0);
-    if (B >= kRmxMinBatch && E <= kRmxMaxE && H % 32 == 0 && H <= kRmxMaxH && vec &&
+    if (lg_ws && rmx_tiled(B, E) && H % 32 == 0 && H <= kRmxMaxH && vec) {
+        // inside the layer, E > 64: the tiled two-pass router (bounds into the workspace);
+        // at config 4 it takes 23 us against 30 for the two-launch exact router, while
+        // with E <= 64 (config 3) k_router_mx is as fast in one launch
+        hipLaunchKernelGGL(k_rmx_bounds, dim3((B + kRmxTok - 1) / kRmxTok, (E + 15) / 16), dim3(kRmxThreads), 0,
+                           stream, (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, B, H, E,
+                           (float2*)lg_ws);
+        if (int rc = check_launch("router bounds")) return rc;
+        hipLaunchKernelGGL(k_rmx_select, dim3((B + kRsWaves - 1) / kRsWaves), dim3(64 * kRsWaves), 0, stream,
+                           (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, B, H, E, K,
+                           (const float2*)lg_ws, (int32_t*)idx, (float*)wts);
+    } else if (B >= kRmxMinBatch && E <= kRmxMaxE && H % 32 == 0 && H <= kRmxMaxH && vec &&
         (E <= 64 || (int64_t)B * E >= 64 * 4096)) {
         // two passes: matrix-core bounds, exact fp64 logits of the candidates only
         const RmxLayout Lr = rmx_layout(H);

@@ -345,13 +345,16 @@ def test_layer_batch1_route_ties_and_nan(oracle):
 
 
 @pytest.mark.parametrize("E,H,K,B", [(128, 256, 4, 100), (128, 2880, 4, 256), (300, 96, 8, 40), (96, 224, 2, 100),
-                                     (64, 256, 4, 100), (32, 2880, 4, 64), (40, 96, 1, 17), (8, 128, 8, 127)])
+                                     (64, 256, 4, 100), (32, 2880, 4, 64), (40, 96, 1, 17), (8, 128, 8, 127),
+                                     (100, 96, 4, 300), (128, 3072, 8, 130), (65, 64, 2, 129)])
 def test_layer_two_launch_router(oracle, E, H, K, B):
     """Mid-size batches (B * E >= 8192 outside the two-pass range) route in two
     launches (logits of 8 tokens x 16 experts per workgroup, then one selection
     workgroup per token); the smaller ones here take k_router. Indices bit-exact and
     weights as the oracle's, with ties to the lower index, a NaN token, more than 256
-    experts (arg-max rounds), k = 1 and k = E."""
+    experts (arg-max rounds), k = 1 and k = E. Batches of 128 or more with 64 < E <= 128
+    take the tiled two-pass router (bounds per 16 x 16 tile, then one selection wave
+    per token), including expert counts that are not multiples of 16."""
     layer = syn.make_layer(E, H, 64, K, seed=E + B)
     tie = [2, 5, 9] if E > 9 else [1, 3, 5]
     rw = layer.router_w.copy()

@@ -310,13 +310,17 @@ def test_layer_streaming_gemv(oracle, E, H, I, K, B, hot, bias):
     _check_layer(oracle, layer, x, f"stream E={E} H={H} I={I} K={K} B={B} hot={hot} bias={bias}")
 
 
-@pytest.mark.parametrize("E,H,I,K", [(32, 2880, 2880, 4), (256, 256, 128, 8), (128, 4096, 256, 4),
-                                     (4, 64, 64, 4), (7, 96, 64, 1)])
-def test_layer_batch1_fused_route(oracle, E, H, I, K):
+@pytest.mark.parametrize("E,H,I,K,bias", [(32, 2880, 2880, 4, True), (256, 256, 128, 8, True),
+                                          (128, 4096, 256, 4, True), (4, 64, 64, 4, True), (7, 96, 64, 1, True),
+                                          (300, 64, 96, 3, True), (32, 2880, 2880, 4, False),
+                                          (16, 160, 2944, 2, True)])
+def test_layer_batch1_fused_route(oracle, E, H, I, K, bias):
     """Batch 1 routes in one launch (router, top-k, softmax and the bucketing of the
     token's k pairs): E up to the 256 limit, k = E, k = 1, a hidden size needing
-    two passes of the row loads (4096)."""
-    layer = syn.make_layer(E, H, I, K, seed=E * 3 + K)
+    two passes of the row loads (4096). With k <= 4 the down projection and the
+    combine run as one launch (k_mx_down1), here also after the general router and
+    bucketing (E = 300), without biases, and at the 92-block K limit (I = 2944)."""
+    layer = syn.make_layer(E, H, I, K, seed=E * 3 + K, with_bias=bias)
     x = syn.make_x(1, H, seed=E + H)
     _check_layer(oracle, layer, x, f"batch-1 route E={E} H={H} I={I} K={K}")
 

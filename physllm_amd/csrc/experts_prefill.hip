@@ -609,28 +609,28 @@ __device__ __forceinline__ u32x4_t rsrc_words(const void* base, uint32_t bytes) 
 }
 
 // Every lane copies the 16 (dma16) or 4 (dma4) bytes at buffer offset voff to LDS at
-// lds_window + 16 * lane (+ 4 * lane); M0 holds the wave-uniform window; loads past
-// the range write zeros. Inline assembly (see above); nothing else in the kernel
-// uses M0.
+// lds_window + 16 * lane (+ 4 * lane); loads past the range write zeros. The
+// wave-uniform window is an M0-bound input operand, so the compiler itself sets M0
+// before the statement and knows its value afterwards (M0 is never clobbered). The
+// s_nop covers the M0-write to LDS-DMA hazard, which the compiler does not see
+// inside the statement.
 __device__ __forceinline__ void dma16(const u32x4_t& r, const lds_u8* lds_window, uint32_t voff) {
     const uint32_t w = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_window);
     asm volatile(
-        "s_mov_b32 m0, %0\n\t"
         "s_nop 0\n\t"
-        "buffer_load_dwordx4 %1, %2, 0 offen lds"
+        "buffer_load_dwordx4 %0, %1, 0 offen lds"
         :
-        : "s"(w), "v"(voff), "s"(r)
-        : "memory", "m0");
+        : "v"(voff), "s"(r), "{m0}"(w)
+        : "memory");
 }
 __device__ __forceinline__ void dma4(const u32x4_t& r, const lds_u8* lds_window, uint32_t voff) {
     const uint32_t w = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_window);
     asm volatile(
-        "s_mov_b32 m0, %0\n\t"
         "s_nop 0\n\t"
-        "buffer_load_dword %1, %2, 0 offen lds"
+        "buffer_load_dword %0, %1, 0 offen lds"
         :
-        : "s"(w), "v"(voff), "s"(r)
-        : "memory", "m0");
+        : "v"(voff), "s"(r), "{m0}"(w)
+        : "memory");
 }
 
 // Waits for every vector-memory load of this wave, the LDS copies included.

@@ -134,9 +134,37 @@ def free_device_memory():
     torch.cuda.empty_cache()
 
 
+def timed_runs(stream, steps: int, call, runs: int = 21):
+    """`runs` runs of `steps` back-to-back calls, each run between its own pair of events
+    on the launch stream; returns each run's ms per step."""
+    import torch
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(runs + 1)]
+    out = []
+    for r in range(runs):
+        torch.cuda.synchronize()
+        evs[0].record(stream)
+        for i in range(steps):
+            call(r * steps + i)
+        evs[r + 1].record(stream)
+        torch.cuda.synchronize()
+        out.append(evs[0].elapsed_time(evs[r + 1]) / steps)
+    return np.array(out)
+
+
+def median_summary(runs_ms, steps: int) -> dict:
+    return {"runs": int(len(runs_ms)), "steps_per_run": int(steps),
+            "ms_per_step_median": round(float(np.median(runs_ms)), 5),
+            "ms_per_step_min": round(float(np.min(runs_ms)), 5),
+            "ms_per_step_max": round(float(np.max(runs_ms)), 5),
+            "note": "value = K-step mean of the timed region; value_median = median over these runs of "
+                    "(run time / K), BASELINE's median of >= 20 runs; per_step_ms brackets every step "
+                    "with its own events, which removes the launch overlap of back-to-back steps"}
+
+
 def summarize(r: dict) -> dict:
     """The by_config entry of one config's result: throughput, time, roofline, CPU baseline."""
-    keep = ("value", "unit", "ms_per_step", "dtype", "config", "roofline", "cpu_baseline")
+    keep = ("value", "value_median", "median_of_runs", "unit", "ms_per_step", "dtype", "config", "roofline",
+            "cpu_baseline")
     out = {k: r[k] for k in keep}
     lay = r.get("layer", {})
     for k in ("per_step_ms", "stage_ms", "hbm_gbs", "hbm_frac"):
@@ -235,8 +263,14 @@ def bench_layer(cfg_i: int, args, cpu_seconds: float) -> dict:
     if graphs:
         assert torch.equal(out, ref_out), "timed replays changed the output"
 
+    # ---- median of runs (BASELINE asks for the median of >= 20 runs): 21 more runs of K
+    # back-to-back steps, each run between its own pair of events; the run's time / K
+    runs_ms = timed_runs(stream, args.steps, lambda i: graphs[i % n_copies].replay() if graphs else step(i))
+
     # ---- per-step spread: K more steps, each between its own pair of events (after the
-    # timed region, so the reported value is not affected); median and 10/90th percentiles
+    # timed region, so the reported value is not affected); median and 10/90th percentiles.
+    # An event between every two steps costs each step part of the launch overlap that
+    # back-to-back steps have, so these per-step times sit above the run means.
     pev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     pev[0].record(stream)
     for i in range(args.steps):
@@ -315,16 +349,22 @@ def bench_layer(cfg_i: int, args, cpu_seconds: float) -> dict:
             by = et * layer.expert_bytes + E * H * 2 + E * 2 + Bs * H * 2 * 2
             out_s = torch.empty((Bs, H), dtype=torch.int16, device="cuda")
             ws_s = torch.empty(dl0.workspace_bytes(Bs), dtype=torch.uint8, device="cuda")
-            for i in range(args.warmup + n_copies):
-                copies[i % n_copies].forward(xs_d, out_s, ws_s, stream=s)
+            # this batch's own rotation: its touched bytes x copies > 1.1 GB
+            nc = max(1, math.ceil(1.1e9 / by))
+            while len(copies) < nc:
+                t = {k: (v.clone() if v is not None else None) for k, v in dl0.tensors.items()}
+                copies.append(ops.DeviceMoELayer.from_tensors(H, I, E, K, t, layer.alpha, layer.limit))
+            for i in range(args.warmup + nc):
+                copies[i % nc].forward(xs_d, out_s, ws_s, stream=s)
             torch.cuda.synchronize()
             evs[0].record(stream)
             for i in range(args.steps):
-                copies[i % n_copies].forward(xs_d, out_s, ws_s, stream=s)
+                copies[i % nc].forward(xs_d, out_s, ws_s, stream=s)
             evs[1].record(stream)
             torch.cuda.synchronize()
             ms_s = evs[0].elapsed_time(evs[1]) / args.steps
-            sweep.append({"batch": Bs, "experts_touched": et, "us_per_step": round(ms_s * 1e3, 2),
+            sweep.append({"batch": Bs, "experts_touched": et, "weight_copies_rotated": nc,
+                          "us_per_step": round(ms_s * 1e3, 2),
                           "tokens_per_s": round(Bs / (ms_s * 1e-3), 1),
                           "hbm_frac": round(by / (ms_s * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
 
@@ -378,6 +418,8 @@ def bench_layer(cfg_i: int, args, cpu_seconds: float) -> dict:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
+        "value_median": round(B / (float(np.median(runs_ms)) * 1e-3), 1),
+        "median_of_runs": median_summary(runs_ms, args.steps),
         "dtype": "bf16",
         "data": "synthetic (seeded; MXFP4 e2m1 codes uniform, E8M0 scales 2^-8..2^-4, bf16 N(0,.02) biases/router, x N(0,1))",
         "config": {"workload": cfgd["workload"] + (f" (at batch {B})" if args.batch else ""),
@@ -440,6 +482,7 @@ def bench_dequant(args, cpu_seconds: float) -> dict:
     wall = time.perf_counter() - t0
     ms = ev0.elapsed_time(ev1) / args.steps
     gbs = alg / (ms * 1e-3) / 1e9
+    runs_ms = timed_runs(stream, args.steps, lambda i: ops.mxfp4_dequant(pd, sd, out, s))
     # per-launch spread (after the timed region): median and 10/90th percentiles
     pev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     pev[0].record(stream)
@@ -502,6 +545,8 @@ def bench_dequant(args, cpu_seconds: float) -> dict:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
+        "value_median": round(alg / (float(np.median(runs_ms)) * 1e-3) / 1e9, 1),
+        "median_of_runs": median_summary(runs_ms, args.steps),
         "dtype": "u8->bf16",
         "data": "synthetic (seeded; e2m1 codes uniform 0-15, E8M0 scales 2^-8..2^-4)",
         "config": {"workload": cfgd["workload"], "config_index": 1, "numel": numel,

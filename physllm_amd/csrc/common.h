@@ -166,4 +166,53 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return rowpair32_sum_f64(v);
 }
 
+// ---- LDS pointers and direct copies into LDS ----------------------------------
+// LDS addresses as 32-bit local pointers
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+template <class T>
+__device__ __forceinline__ T lds_ld(const lds_u8* q) {
+    return *(const __attribute__((address_space(3))) T*)q;
+}
+template <class T>
+__device__ __forceinline__ void lds_st(lds_u8* q, T v) {
+    *(__attribute__((address_space(3))) T*)q = v;
+}
+
+// The four words of a raw buffer descriptor over [base, base + bytes) (stride 0, the
+// flags word of make_rsrc above), in scalar registers.
+__device__ __forceinline__ u32x4_t rsrc_words(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return u32x4_t{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
+                   (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu),
+                   (uint32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000u};
+}
+
+// Every lane copies the 16 (dma16) or 4 (dma4) bytes at buffer offset voff to LDS at
+// lds_window + 16 * lane (+ 4 * lane); loads past the range write zeros. The
+// wave-uniform window is an M0-bound input operand, so the compiler itself sets M0
+// before the statement and knows its value afterwards (M0 is never clobbered). The
+// s_nop covers the M0-write to LDS-DMA hazard, which the compiler does not see
+// inside the statement.
+__device__ __forceinline__ void dma16(const u32x4_t& r, const lds_u8* lds_window, uint32_t voff) {
+    const uint32_t w = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_window);
+    asm volatile(
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %0, %1, 0 offen lds"
+        :
+        : "v"(voff), "s"(r), "{m0}"(w)
+        : "memory");
+}
+__device__ __forceinline__ void dma4(const u32x4_t& r, const lds_u8* lds_window, uint32_t voff) {
+    const uint32_t w = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_window);
+    asm volatile(
+        "s_nop 0\n\t"
+        "buffer_load_dword %0, %1, 0 offen lds"
+        :
+        : "v"(voff), "s"(r), "{m0}"(w)
+        : "memory");
+}
+
+// Waits for every vector-memory load of this wave, the LDS copies included.
+__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 }  // namespace physllm

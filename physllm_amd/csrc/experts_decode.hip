@@ -375,248 +375,251 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p, const in
 }
 
 // ---------------------------------------------------------------------------
-// Streaming form (decode with many touched experts). One 8-wave workgroup per
-// CU walks a round-robin share of work items (pass-table entry, K split, 128-row
-// set): at most 16 tokens of one expert against 128 weight rows; wave w owns
-// rows 16w..16w+15 of the set. The 23 weight stripes of a tile sit in a
-// circular register buffer: right after k-step j of the current item has been
-// decoded, register j is refilled with k-step j of the next item, so every wave
-// keeps 23 16-byte loads in flight at all times (a load-then-compute schedule
-// leaves the HBM queues idle while the matrix cores work). The next item's
-// scales, biases and — when its token chunk or K split differs — activation
-// rows are loaded at the start of the current item, ahead of its refills, and
-// written to LDS at its end; loads that are not needed use an empty buffer
-// range (zeros, no memory traffic), so every item issues the same loads in the
-// same order and no wait ever covers a refill that is not yet needed.
+// Streaming form (decode with many touched experts): persistent, one 4-wave
+// workgroup per CU, so each SIMD runs a single wave.
+//
+// A read-only model of this loop (persistent groups, a 23-stripe register ring
+// per wave, the k-steps' LDS reads, conversions and MFMAs) streams 1.1 GB at
+// 6.2 TB/s with 4 waves per CU, 5.75 with 8 and 5.1-5.3 with 12 or 16: a second
+// wave on a SIMD does not hide the k-step latency, it competes with the first
+// for issue slots, LDS and the load-return path.
+//
+// Work items are (pass entry, 64-row set) in entry-major order, so the row sets of
+// one 16-token chunk of one expert are consecutive. Workgroup b takes one
+// contiguous range of items (all ranges within one item of each other), and the
+// ranges of the workgroups of one XCD (b % 8) are consecutive: the chunks of one
+// expert run on one XCD at about the same time and meet in its L2.
+//  - The 16 activation rows of the current entry stay in LDS. A workgroup copies
+//    them in (direct copies into LDS, no registers) at its start and again only
+//    when its range crosses into the next entry, about once per workgroup. Unit c
+//    of staged row q sits at unit c ^ q, so the 16 token rows of an MFMA fragment
+//    read hit 16 different bank groups.
+//  - Each wave keeps its 16 rows x 23 k-steps in a circular register buffer:
+//    right after k-step j of the current item is decoded, register j is
+//    reloaded with k-step j of the next item (23 loads in flight per wave).
+//  - The next item's scales and biases load at the start of the current item,
+//    ahead of its refills; the scales go to a wave-private LDS slice.
+//  - Outputs go to a wave-private LDS ring, written to memory in bursts (ring
+//    full, and at the start of the workgroup's last item). A store sits in the
+//    in-order vector-memory counter: every load issued after it counts as
+//    complete only once the store is acknowledged, which under the read stream
+//    takes longer than an item. Per-item stores cost 12% at the GPT-OSS-120B
+//    shape (decode batch 256).
 // ---------------------------------------------------------------------------
-constexpr int kStreamWaves = 8;
+constexpr int kStreamWaves = 4;
 constexpr int kStreamThreads = 64 * kStreamWaves;
-constexpr int kSetRows = 16 * kStreamWaves;
-constexpr int kStreamRowLoads = 6;  // 64-unit loads per staged row: K ranges of <= 384 units (96 blocks)
-constexpr int kStreamRowStride = 64 * kStreamRowLoads + 1;  // LDS row stride of the staged activations
-// bytes of one wave's scale slice in the streaming kernel: the 128 16-byte units
-// its lanes store (the tile's 16 x NB <= 1536 bytes, then unread padding)
-constexpr int kStreamSclSlice = 128 * 16;
-constexpr int kStreamMaxNB = 96;    // a tile's scales (16 x NB bytes) fit in the first 1536 bytes of the slice
+constexpr int kStreamSetRows = 16 * kStreamWaves;                  // weight rows per item
+constexpr int kStreamMaxNB = 4 * kGemvNit;                         // K <= 2944: the 23 k-steps of a tile
+constexpr int kStreamActUnits = 384;                               // 16-byte units per staged row (>= K/8)
+constexpr int kStreamActBytes = kPassRows * kStreamActUnits * 16;  // 96 KiB
+constexpr int kStreamSlice = 2048;                                 // a wave's scale slice: 16 x NB bytes
+constexpr int kStreamOutWave = 12 * 1024;                          // a wave's output ring
+constexpr int kStreamLds = kStreamActBytes + 2 * kStreamWaves * kStreamSlice + kStreamWaves * kStreamOutWave;
+static_assert(kStreamLds <= 160 * 1024, "streaming GEMV LDS");
+static_assert(4 * kStreamMaxNB <= kStreamActUnits && 16 * kStreamMaxNB <= kStreamSlice, "streaming GEMV tiles");
 
-struct StreamItem {
-    int e, ne, p0, kb0, nblk, split, r0, key;  // key: pass entry and split (same key = same activations)
-};
-
-// Work item f: the items of an expert with np token chunks are numbered
-// ((split * sets) + set) * np + chunk, so an expert's chunks run back to back on
-// the same weight tile (re-reads hit L2) and single-chunk experts step through
-// row sets with the same activations.
-__device__ __forceinline__ StreamItem stream_item(const GemvParams& p, const int4* __restrict__ passes, int f,
-                                                  int sets, int per, int NB, int wave) {
-    const int ipe = sets * p.split;  // items per chunk
-    const int u = f / ipe;           // some chunk of f's expert
-    const int4 pu = passes[u];
-    const int first = u - (pu.w & 0xffff), np = pu.w >> 16;
-    const int l = f - first * ipe;
-    const int chunk = l % np;
-    const int rest = l / np;
-    const int split = rest / sets;
-    const int set = rest - split * sets;
-    const int entry = first + chunk;
-    const int4 pe = passes[entry];
-    StreamItem it;
-    it.e = pe.x;
-    it.ne = pe.y;
-    it.p0 = pe.z;
-    it.split = split;
-    it.kb0 = min(NB, split * per);
-    it.nblk = min(NB, it.kb0 + per) - it.kb0;
-    it.r0 = set * kSetRows + wave * 16;
-    it.key = entry * p.split + split;
-    return it;
-}
-
-// The k-steps of one item in the 16-token streaming GEMV: decode k-step j of the
-// tile in wq[j] against the staged activations, then load k-step j of the next
-// item's tile into wq[j] right after its last read.
-__device__ __forceinline__ void stream_steps(u32x4_t (&wq)[kGemvNit], f32x4_t& acc0, f32x4_t& acc1, f32x4_t& acc2,
-                                             f32x4_t& acc3, const uint8_t* sl, const uint4* xl, int nblk, int g,
-                                             __amdgpu_buffer_rsrc_t rsrc, uint32_t svoff) {
-#pragma unroll
-    for (int j = 0; j < kGemvNit; ++j) {
-        if (4 * j < nblk) {  // wave-uniform
-            const bool edge = 4 * j + 3 >= nblk;
-            const bool bv = 4 * j + g < nblk;
-            uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
-            asm volatile("" : "+v"(sj));
-            const float sf = e8m0_scale_operand(sj);
-            u32x4_t q = wq[j];
-            uint4 x0 = xl[16 * j + 0], x1 = xl[16 * j + 1], x2 = xl[16 * j + 2], x3 = xl[16 * j + 3];
-            if (edge && !bv) {
-                q = u32x4_t{0u, 0u, 0u, 0u};
-                x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
-            }
-            acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
-            acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
-            acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
-            acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
-        }
-        // refill after the last read of wq[j]: the load reuses its registers
-        wq[j] = buf_load16(rsrc, svoff, 64 * j);
-        __builtin_amdgcn_sched_barrier(0);  // one refill per k-step
-    }
-}
-
-// The pass table, sorted pair ids and outputs come in as restrict kernel
-// arguments: the output stores then provably leave the tables alone and the
-// per-item table reads compile to scalar loads, which a wave does not have to
-// order behind its in-flight weight loads.
 template <int MODE>
 __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p, const int4* __restrict__ passes,
                                                                    const int32_t* __restrict__ perm,
                                                                    const int32_t* __restrict__ n_passes,
                                                                    void* __restrict__ out) {
     extern __shared__ uint4 lds[];
-    const int NB = p.Kdim >> 5;
-    const int per = (NB + p.split - 1) / p.split;  // <= 92 and NB <= 96: checked by the launcher
-    const int sets = (p.R + kSetRows - 1) / kSetRows;
-    const int total = *n_passes * p.split * sets;
-    // round-robin items, XCD-aware: workgroup b (XCD b % 8) takes items i(b) + k * G
-    // with i(b) = (b % 8) * (G / 8) + b / 8, so items next to each other in the
-    // order (the chunks of one weight tile, the row sets of one expert) run at the
-    // same time on one XCD and share its L2
-    // G: the fewest workgroups (a multiple of 8, at most the grid) that still take at
-    // most ceil(total / grid) items each, so no workgroup runs one item more than most:
-    // at config 2 (1,620 gate_up items, 828 down items on 256 CUs) 232 and 208 of them
-    // (a last round on 84 or 60 CUs costs nearly a full item time)
-    if (total <= 0) return;
-    const int per_wg = (total + (int)gridDim.x - 1) / (int)gridDim.x;
-    const int G = min((int)gridDim.x, ((total + per_wg - 1) / per_wg + 7) & ~7);
-    if ((int)blockIdx.x >= G) return;
-    const int f0 = (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3), fstep = G;
-    if (f0 >= total) return;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int NB = p.Kdim >> 5;       // <= kStreamMaxNB (launcher)
+    const int ku = p.Kdim >> 3;       // 16-byte activation units per row, <= kStreamActUnits
+    const int sets = (p.R + kStreamSetRows - 1) / kStreamSetRows;
+    const int total = *n_passes * sets;
+    const int G = (int)gridDim.x;     // a multiple of 8
+    const int rix = (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3);
+    const int f0 = (int)((int64_t)total * rix / G), f1 = (int)((int64_t)total * (rix + 1) / G);
+    if (f0 >= f1) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & (kStreamWaves - 1);
     const int lane = threadIdx.x & 63;
     const int m = lane & 15, g = lane >> 4;
-    // LDS activation row stride in 16-byte units: every staged row holds all 6 x 64 units a
-    // thread loads (units past the K range are never read), plus one unit of pad (odd stride)
-    const int su = kStreamRowStride;
     const uint32_t row_bytes = (uint32_t)(p.Kdim >> 1);
     const uint32_t exp_w = (uint32_t)p.R * row_bytes;
     const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;
     const uint32_t exp_b = p.bias ? (uint32_t)p.R * 2u : 0u;  // empty range: the bias reads as zero
     const uint32_t act_bytes = (uint32_t)p.act_rows * (uint32_t)p.Kdim * 2u;
-    uint4* xs = lds;                                                     // [16][su]
-    uint8_t* scl0 = (uint8_t*)(lds + kPassRows * su) + wave * kStreamSclSlice;  // [2 bufs][8 waves][slice]
-    constexpr int kSclBuf = kStreamWaves * kStreamSclSlice;
+    constexpr uint32_t kPast = 0x80000000u;  // an offset past every range: zeros
+    lds_u8* act = (lds_u8*)lds;
+    uint8_t* slice0 = (uint8_t*)lds + kStreamActBytes + wave * kStreamSlice;  // [2 buffers][4 waves][kStreamSlice]
+    constexpr int kSliceBuf = kStreamWaves * kStreamSlice;
 
-    // loads of one item's side data: 16 rows of scales, this lane's 4 biases and
-    // (when `act` is set) the item's activation rows 2w, 2w+1 — as 64-unit
-    // lane-contiguous runs at immediate offsets from one scalar row offset
+    // the 16 activation rows of pass entry pe into LDS: wave w copies rows 4w..4w+3,
+    // 6 copies of 64 units per row (units past K and rows past the entry's tokens
+    // read zeros)
+    auto stage_act = [&](int4 pe) {
+        const u32x4_t ra = rsrc_words(p.act, act_bytes);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int q = 4 * wave + rr;
+            const int row = q < pe.y ? ((MODE == kModeGateUp) ? perm[pe.z + q] / p.top_k : pe.z + q) : -1;
+#pragma unroll
+            for (int k = 0; k < kStreamActUnits / 64; ++k) {
+                const int c = (64 * k + lane) ^ q;  // source unit of destination unit 64k + lane
+                const uint32_t voff =
+                    (row >= 0 && c < ku) ? (uint32_t)row * (uint32_t)(p.Kdim * 2) + (uint32_t)c * 16u : kPast;
+                dma16(ra, act + (q * kStreamActUnits + 64 * k) * 16, voff);
+            }
+        }
+    };
     u32x4_t sv0, sv1;
     uint2 bnx;
-    u32x4_t av[2][kStreamRowLoads];
-    auto side_load = [&](const StreamItem& it, bool act) {
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales + (size_t)it.e * exp_s, exp_s);
-        sv0 = buf_load16(rs, (uint32_t)it.r0 * NB + lane * 16u, 0);
-        sv1 = buf_load16(rs, (uint32_t)it.r0 * NB + lane * 16u, 1024);
-        const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.bias + (size_t)it.e * p.R, it.split == 0 ? exp_b : 0u);
-        const u32x2_t b2 = __builtin_amdgcn_raw_buffer_load_b64(rb, (uint32_t)(it.r0 + 4 * g) * 2u, 0, 0);
+    auto side_load = [&](int e, int r0, bool live) {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales + (size_t)e * exp_s, live ? exp_s : 0u);
+        sv0 = buf_load16(rs, (uint32_t)r0 * NB + lane * 16u, 0);
+        sv1 = buf_load16(rs, (uint32_t)r0 * NB + lane * 16u, 1024);
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.bias + (size_t)e * p.R, live ? exp_b : 0u);
+        const u32x2_t b2 = __builtin_amdgcn_raw_buffer_load_b64(rb, (uint32_t)(r0 + 4 * g) * 2u, 0, 0);
         bnx = make_uint2(b2[0], b2[1]);
-        const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.act, act ? act_bytes : 0u);
-#pragma unroll
-        for (int r2 = 0; r2 < 2; ++r2) {
-            const int q = min(2 * wave + r2, it.ne - 1);
-            const int row = (MODE == kModeGateUp) ? perm[it.p0 + q] / p.top_k : it.p0 + q;
-            // rows past the item's tokens are never read: load them from past the range
-            // (zeros, no memory request; the 6 immediate offsets keep it below 2^32)
-            const uint32_t voff = 2 * wave + r2 < it.ne
-                                      ? (uint32_t)row * (uint32_t)(p.Kdim * 2) + (uint32_t)(it.kb0 * 4 + lane) * 16u
-                                      : 0x80000000u;
-#pragma unroll
-            for (int u = 0; u < kStreamRowLoads; ++u) av[r2][u] = buf_load16(ra, voff, 1024 * u);
-        }
     };
-    // wave-private slice: no barrier. Every lane stores both units (the slice holds
-    // 128; units past the tile's 16 x NB bytes are never read): a store under
-    // `lane < NB` lets the compiler sink the scale load into that branch, behind
-    // the item's weight stripes, and wait for all of them.
+    // wave-private slice, no barrier. Every lane stores both units (units past the
+    // tile's 16 x NB bytes are never read): a store under a lane test lets the
+    // compiler sink the scale load into that branch, behind the item's stripes,
+    // and wait for all of them.
     auto scale_store = [&](int b) {
-        uint8_t* s = scl0 + b * kSclBuf;
-        ((u32x4_t*)s)[lane] = sv0;
-        ((u32x4_t*)s)[lane + 64] = sv1;
-    };
-    // unconditional stores: rows past the item's tokens hold zeros and units
-    // past its K range hold the next row's elements, and neither is ever read
-    auto act_store = [&]() {
-        __syncthreads();  // every wave has finished reading the previous activations
-#pragma unroll
-        for (int r2 = 0; r2 < 2; ++r2) {
-            const int r = 2 * wave + r2;
-#pragma unroll
-            for (int u = 0; u < kStreamRowLoads; ++u) ((u32x4_t*)xs)[r * su + lane + 64 * u] = av[r2][u];
-        }
-        __syncthreads();
-    };
-    auto wrsrc = [&](const StreamItem& it, bool live) {
-        return make_rsrc(p.blocks + (size_t)it.e * exp_w, live ? exp_w : 0u);
-    };
-    auto woffs = [&](const StreamItem& it) {
-        return (uint32_t)(it.r0 + m) * row_bytes + (uint32_t)(it.kb0 + g) * 16u;
+        uint8_t* sb = slice0 + b * kSliceBuf;
+        ((u32x4_t*)sb)[lane] = sv0;
+        ((u32x4_t*)sb)[lane + 64] = sv1;
     };
 
-    // prologue: the first item's side data, then its weights — the order of the
-    // steady state (an item's side data is issued before its stripes), so the
-    // staging below waits only for the small loads and the k-loop (which issues
-    // the next item's loads) starts while the stripes stream in
-    StreamItem cur = stream_item(p, passes, f0, sets, per, NB, wave);
-    side_load(cur, true);
+    // a pass-table entry, wave-uniform
+    auto entry = [&](int u) -> int4 {
+        const int4 v = passes[u];
+        return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                         __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+    };
+    auto item_at = [&](int f) -> int2 {  // {entry, set}: entry-major
+        const int u = f / sets;
+        return make_int2(u, f - u * sets);
+    };
+    // this wave's output ring: per item and lane 4 bytes (two bf16 of h) or 16 (four
+    // fp32 of y), from item fa on; flush(fb) writes items fa .. fb - 1 to memory
+    constexpr int kOutLane = (MODE == kModeGateUp) ? 4 : 16;
+    constexpr int kOutCap = kStreamOutWave / (64 * kOutLane);
+    uint8_t* oring =
+        (uint8_t*)lds + kStreamActBytes + 2 * kStreamWaves * kStreamSlice + wave * kStreamOutWave + lane * kOutLane;
+    int fa = f0;  // first staged item
+    auto flush = [&](int fb) {
+        for (int ff = fa; ff < fb; ++ff) {
+            const int2 it2 = item_at(ff);
+            const int e2 = it2.x, s2 = it2.y;
+            const int4 q2 = entry(e2);
+            const int r2 = s2 * kStreamSetRows + 16 * wave;
+            const uint8_t* src = oring + (ff - fa) * (64 * kOutLane);
+            if (r2 < p.R && m < q2.y) {
+                const int pp = q2.z + m;
+                const int rr = r2 + 4 * g;
+                if (MODE == kModeGateUp) {
+                    uint32_t* hout = (uint32_t*)((uint16_t*)out + (size_t)pp * (p.R >> 1) + (rr >> 1));
+                    *hout = *(const uint32_t*)src;
+                } else {
+                    *(float4*)((float*)out + (size_t)pp * p.R + rr) = *(const float4*)src;
+                }
+            }
+        }
+        fa = fb;
+    };
+    const int2 it0 = item_at(f0);
+    int en = it0.x, s = it0.y;
+    int4 pe = entry(en);
+    stage_act(pe);
+    side_load(pe.x, s * kStreamSetRows + 16 * wave, true);
     u32x4_t wq[kGemvNit];
     {
-        const __amdgpu_buffer_rsrc_t rw = wrsrc(cur, true);
-        const uint32_t voff = woffs(cur);
+        const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.blocks + (size_t)pe.x * exp_w, exp_w);
+        const uint32_t voff = (uint32_t)(s * kStreamSetRows + 16 * wave + m) * row_bytes + (uint32_t)g * 16u;
 #pragma unroll
         for (int j = 0; j < kGemvNit; ++j) wq[j] = buf_load16(rw, voff, 64 * j);
     }
     uint2 bcur = bnx;
     scale_store(0);
-    act_store();
+    // the activation copies (issued first, and not counted by the compiler's waits):
+    // at most the 2 scale loads, the bias load and the 23 stripes may still be in flight
+    asm volatile("s_waitcnt vmcnt(26)" ::: "memory");
+    __syncthreads();
     int buf = 0;
+    // this lane's activation fragment i of k-step j: unit 16j + ((4g + i) ^ m) of row m
+    const uint4* xrow = (const uint4*)lds + m * kStreamActUnits;
+    const int xo0 = (4 * g + 0) ^ m, xo1 = (4 * g + 1) ^ m, xo2 = (4 * g + 2) ^ m, xo3 = (4 * g + 3) ^ m;
 
-    for (int f = f0; f < total; f += fstep) {
-        const bool has_next = f + fstep < total;
-        const StreamItem nxt = stream_item(p, passes, has_next ? f + fstep : f, sets, per, NB, wave);
-        const bool restage = has_next && nxt.key != cur.key;
-        side_load(nxt, restage);
-        const __amdgpu_buffer_rsrc_t rsrc = wrsrc(nxt, has_next);
-        const uint32_t svoff = woffs(nxt);
-        const uint8_t* sl = scl0 + buf * kSclBuf + m * NB + cur.kb0 + g;
-        const uint4* xl = xs + min(m, cur.ne - 1) * su + 4 * g;
+    for (int f = f0; f < f1; ++f) {
+        const bool has_next = f + 1 < f1;
+        if (!has_next) flush(f);  // the staged outputs go out while the last item computes
+        const int2 itn = has_next ? item_at(f + 1) : make_int2(en, s);
+        const int en_n = itn.x, s_n = itn.y;
+        const int4 pe_n = (has_next && en_n != en) ? entry(en_n) : pe;
+        const int r0 = s * kStreamSetRows + 16 * wave;
+        const int r0_n = s_n * kStreamSetRows + 16 * wave;
+        side_load(pe_n.x, r0_n, has_next);
+        const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(p.blocks + (size_t)pe_n.x * exp_w, has_next ? exp_w : 0u);
+        const uint32_t svoff = (uint32_t)(r0_n + m) * row_bytes + (uint32_t)g * 16u;
+        const uint8_t* sl = slice0 + buf * kSliceBuf + m * NB + g;
         f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
-        stream_steps(wq, acc0, acc1, acc2, acc3, sl, xl, cur.nblk, g, rsrc, svoff);
-        if (cur.r0 < p.R && m < cur.ne) {
+#pragma unroll
+        for (int j = 0; j < kGemvNit; ++j) {
+            if (4 * j < NB) {  // wave-uniform
+                const bool edge = 4 * j + 3 >= NB;
+                const bool bv = 4 * j + g < NB;
+                uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
+                asm volatile("" : "+v"(sj));
+                const float sf = e8m0_scale_operand(sj);
+                u32x4_t q = wq[j];
+                uint4 x0 = xrow[16 * j + xo0], x1 = xrow[16 * j + xo1], x2 = xrow[16 * j + xo2],
+                      x3 = xrow[16 * j + xo3];
+                if (edge && !bv) {
+                    q = u32x4_t{0u, 0u, 0u, 0u};
+                    x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
+                }
+                acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
+                acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
+                acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
+                acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
+            }
+            wq[j] = buf_load16(rsrc, svoff, 64 * j);
+            __builtin_amdgcn_sched_barrier(0);  // one refill per k-step
+        }
+        {
             const f32x4_t acc = (acc0 + acc1) + (acc2 + acc3);
-            const int pp = cur.p0 + m;
-            const int rr = cur.r0 + 4 * g;
             const float b0 = bf16_lo(bcur.x), b1 = bf16_hi(bcur.x), b2 = bf16_lo(bcur.y), b3 = bf16_hi(bcur.y);
+            uint32_t hv = 0;
+            float4 y;
             if (MODE == kModeGateUp) {
                 const float h0 = swiglu(acc[0] + b0, acc[1] + b1, p.alpha, p.limit);
                 const float h1 = swiglu(acc[2] + b2, acc[3] + b3, p.alpha, p.limit);
-                const int I = p.R >> 1;
-                uint32_t* hout = (uint32_t*)((uint16_t*)out + (size_t)pp * I + (rr >> 1));
-                *hout = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
+                hv = f32_to_bf16(h0) | (f32_to_bf16(h1) << 16);
             } else {
-                float4 y;
                 y.x = acc[0] + b0;
                 y.y = acc[1] + b1;
                 y.z = acc[2] + b2;
                 y.w = acc[3] + b3;
-                float* ybase = (float*)out + (size_t)cur.split * p.n_pairs * p.R;
-                *(float4*)(ybase + (size_t)pp * p.R + rr) = y;
+            }
+            if (has_next) {
+                uint8_t* dst = oring + (f - fa) * (64 * kOutLane);
+                if (MODE == kModeGateUp) *(uint32_t*)dst = hv;
+                else *(float4*)dst = y;
+            } else if (r0 < p.R && m < pe.y) {
+                const int pp = pe.z + m;
+                const int rr = r0 + 4 * g;
+                if (MODE == kModeGateUp) *(uint32_t*)((uint16_t*)out + (size_t)pp * (p.R >> 1) + (rr >> 1)) = hv;
+                else *(float4*)((float*)out + (size_t)pp * p.R + rr) = y;
             }
         }
         if (!has_next) break;
+        if (f + 1 - fa == kOutCap) flush(f + 1);
         buf ^= 1;
         scale_store(buf);
         bcur = bnx;
-        if (restage) act_store();
-        cur = nxt;
+        if (en_n != en) {
+            // the next item starts a new pass entry: its activation rows replace these
+            __syncthreads();  // every wave has finished reading the current rows
+            stage_act(pe_n);
+            wait_vmem_all();
+            __syncthreads();
+        }
+        en = en_n;
+        s = s_n;
+        pe = pe_n;
     }
 }
 
@@ -806,7 +809,7 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
     const int rows_per_set = (kGemvThreads / 64) * 16;
     const int sets = (p.R + rows_per_set - 1) / rows_per_set;
     const int n_cu = device_cu_count();
-    const long stream_items = (long)((p.R + kSetRows - 1) / kSetRows) * max_slots * p.split;
+    const long stream_items = (long)((p.R + kStreamSetRows - 1) / kStreamSetRows) * max_slots * p.split;
     const bool fast = per <= 4 * kGemvNit && NB <= kStreamMaxNB;
     // The streaming kernel takes whole K rows (no split: it loads the 23 k-steps of
     // a tile as one row segment) of experts below 2 GiB (32-bit buffer offsets).
@@ -815,13 +818,12 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
         // many touched experts: persistent streaming kernel, one 8-wave group per CU
         // (a multiple of 8 groups: the item order is XCD-aware)
         const unsigned grid = (unsigned)((n_cu + 7) & ~7);
-        const size_t lds = (size_t)kPassRows * kStreamRowStride * 16 + (size_t)2 * kStreamWaves * kStreamSclSlice;
         p.rt = 1;
         if (mode == kModeGateUp)
-            hipLaunchKernelGGL(k_mx_gemv_stream<kModeGateUp>, dim3(grid), dim3(kStreamThreads), lds, stream, p,
+            hipLaunchKernelGGL(k_mx_gemv_stream<kModeGateUp>, dim3(grid), dim3(kStreamThreads), kStreamLds, stream, p,
                                p.passes, p.perm, p.n_passes, p.out);
         else
-            hipLaunchKernelGGL(k_mx_gemv_stream<kModeDown>, dim3(grid), dim3(kStreamThreads), lds, stream, p,
+            hipLaunchKernelGGL(k_mx_gemv_stream<kModeDown>, dim3(grid), dim3(kStreamThreads), kStreamLds, stream, p,
                                p.passes, p.perm, p.n_passes, p.out);
     } else if (fast) {
         // activation units one thread stages per pass: ntok rows x 4*per 16-byte units

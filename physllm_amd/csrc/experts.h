@@ -20,8 +20,9 @@ struct GemvParams {
     const int4* slots;       // [E] {expert, tokens, first sorted position, 0}; tokens = 0 past the touched ones
     const int32_t* n_slots;  // [1] number of touched experts
     const int4* passes;      // [<= N/16 + E] {expert, tokens <= 16, first sorted position, chunk | chunks << 16}:
-                             // each touched expert's tokens in chunks of kPassRows, in slot order (decode only)
-    const int32_t* n_passes; // [1]
+                             // each touched expert's tokens in chunks of kPassRows (decode only); the entries
+                             // of experts with two or more chunks first, then the others, each in expert order
+    const int32_t* n_passes; // [2] {entries, entries of multi-chunk experts}
     void* out;               // gate_up: h bf16 [N, R/2]; down: y fp32 [N, R] (by sorted position)
     int act_rows;            // rows of act (gate_up: batch; down: N)
     int Kdim;                // reduction length (H for gate_up, I for down)

@@ -427,10 +427,34 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
     const int NB = p.Kdim >> 5;       // <= kStreamMaxNB (launcher)
     const int ku = p.Kdim >> 3;       // 16-byte activation units per row, <= kStreamActUnits
     const int sets = (p.R + kStreamSetRows - 1) / kStreamSetRows;
-    const int total = *n_passes * sets;
     const int G = (int)gridDim.x;     // a multiple of 8
     const int rix = (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3);
-    const int f0 = (int)((int64_t)total * rix / G), f1 = (int)((int64_t)total * (rix + 1) / G);
+    // this workgroup's items f in [f0, f1): entry ebase + f / sets, row set f % sets
+    int ebase, f0, f1;
+    {
+        const int npass = n_passes[0], nm = n_passes[1];
+        // an entry of an expert with several chunks gets P workgroups of its own, each
+        // a 1/P share of its row sets; rix = part * nm + entry, so the chunks of one
+        // expert (adjacent entries) run on one XCD, start together and read the same
+        // rows at the same time (one HBM read, the rest L2 hits). The single-chunk
+        // entries share the other workgroups in contiguous ranges.
+        int P = (nm > 0 && npass <= G) ? max(1, (G + npass / 2) / npass) : 0;
+        if (P > 0) P = min(min(P, G / nm), sets);
+        if (P > 0 && npass > nm && G - P * nm < 1) P = (G - 1) / nm;
+        const int M = P * nm;
+        if (rix < M) {
+            const int part = rix / nm;
+            ebase = rix - part * nm;
+            f0 = part * sets / P;
+            f1 = (part + 1) * sets / P;
+        } else {
+            const int e0 = P > 0 ? nm : 0;
+            const int total = (npass - e0) * sets, g = G - M, r = rix - M;
+            ebase = e0;
+            f0 = (int)((int64_t)total * r / g);
+            f1 = (int)((int64_t)total * (r + 1) / g);
+        }
+    }
     if (f0 >= f1) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & (kStreamWaves - 1);
     const int lane = threadIdx.x & 63;
@@ -489,9 +513,9 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
         return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
                          __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
     };
-    auto item_at = [&](int f) -> int2 {  // {entry, set}: entry-major
+    auto item_at = [&](int f) -> int2 {  // {entry, set}
         const int u = f / sets;
-        return make_int2(u, f - u * sets);
+        return make_int2(ebase + u, f - u * sets);
     };
     // this wave's output ring: per item and lane 4 bytes (two bf16 of h) or 16 (four
     // fp32 of y), from item fa on; flush(fb) writes items fa .. fb - 1 to memory

@@ -138,7 +138,7 @@ static Workspace carve(const physllm_moe_config& c, int B, char* base) {
     w.tprefix = (int32_t*)take((E + 1) * 4);
     const bool decode = !use_gemm(c, B);
     w.passes = (int4*)take(decode ? (N / kPassRows + std::min(N, E)) * 16 : 0);
-    w.n_passes = (int32_t*)take(4);
+    w.n_passes = (int32_t*)take(8);  // {entries, entries of multi-chunk experts}
     w.perm = (int32_t*)take(N * 4);
     w.pos = (int32_t*)take(N * 4);
     w.bhist = (int32_t*)take(bucket_hist_bytes((int)N, (int)E));

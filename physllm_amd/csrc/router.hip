@@ -198,7 +198,8 @@ __global__ __launch_bounds__(kRoute1Threads) void k_route1(
     }
     if (lane == 0) {
         *n_slots = K;
-        *n_passes = K;
+        n_passes[0] = K;
+        n_passes[1] = 0;
         offsets[E] = K;
     }
     // counts[e] = 1 for the selected experts, offsets[e] = #{selected < e}; later slots cleared
@@ -906,6 +907,37 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sbuf, int n) {
     return base + x - mine;
 }
 
+// The pass table (decode GEMV work list): each touched expert's sorted positions in
+// chunks of kPassRows, {expert, tokens, first position, chunk index | chunk count
+// << 16}. Entries of experts with two or more chunks come first, then those of the
+// single-chunk experts, each group in expert order; n_passes = {entries, entries of
+// multi-chunk experts}. Called by every thread of the workgroup: thread tid < E owns
+// expert tid, with c pairs from sorted position ex (chunk counts stay below 2^16: the
+// GEMV path has fewer than 64 E pairs).
+__device__ __forceinline__ void write_pass_table(int c, int ex, int E, int* sbuf, int4* __restrict__ passes,
+                                                 int32_t* __restrict__ n_passes) {
+    const int tid = threadIdx.x;
+    const int np = (c + kPassRows - 1) / kPassRows;
+    const int mex = block_excl_scan(np > 1 ? np : 0, sbuf, E);
+    const int sex = block_excl_scan(np == 1 ? 1 : 0, sbuf, E);
+    if (tid == E - 1) {
+        sbuf[0] = mex + (np > 1 ? np : 0);
+        sbuf[1] = sex + (np == 1 ? 1 : 0);
+    }
+    __syncthreads();
+    const int nmulti = sbuf[0], nsingle = sbuf[1];
+    if (tid < E) {
+        const int base = np > 1 ? mex : nmulti + sex;
+        for (int t = 0; t < np; ++t)
+            passes[base + t] = make_int4(tid, min(kPassRows, c - t * kPassRows), ex + t * kPassRows, t | (np << 16));
+    }
+    if (tid == 0 && n_passes) {
+        n_passes[0] = nmulti + nsingle;
+        n_passes[1] = nmulti;
+    }
+    __syncthreads();  // sbuf may be reused
+}
+
 // The body of k_bucket_chunked, called by the whole workgroup: idx (global or
 // LDS) holds the N pairs' experts; smem is the scratch of bucket_smem_bytes(E).
 __device__ __forceinline__ void bucket_chunked_block(const int32_t* idx, int N, int E, int* smem,
@@ -955,18 +987,7 @@ __device__ __forceinline__ void bucket_chunked_block(const int32_t* idx, int N, 
                 if (tid < E && c > 0) tprefix[na] = tex;
                 if (tid == E - 1) tprefix[ntouched] = tex + nt;
             }
-            if (passes) {
-                // each touched expert's sorted positions in chunks of kPassRows:
-                // {expert, tokens, first position, chunk index | chunk count << 16}
-                // (chunk counts stay below 2^16: the GEMV path has < 64 E pairs)
-                const int np = (c + kPassRows - 1) / kPassRows;
-                const int pex = block_excl_scan(np, scan, E);
-                if (tid < E)
-                    for (int t = 0; t < np; ++t)
-                        passes[pex + t] =
-                            make_int4(tid, min(kPassRows, c - t * kPassRows), ex + t * kPassRows, t | (np << 16));
-                if (tid == E - 1 && n_passes) *n_passes = pex + np;
-            }
+            if (passes) write_pass_table(c, ex, E, scan, passes, n_passes);
         }
     }
     __syncthreads();
@@ -1125,18 +1146,7 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_waves(const int32_t* 
                 if (tid < E && c > 0) tprefix[na] = tex;
                 if (tid == E - 1) tprefix[ntouched] = tex + nt;
             }
-            if (passes) {
-                // each touched expert's sorted positions in chunks of kPassRows:
-                // {expert, tokens, first position, chunk index | chunk count << 16}
-                // (chunk counts stay below 2^16: the GEMV path has < 64 E pairs)
-                const int np = (c + kPassRows - 1) / kPassRows;
-                const int pex = block_excl_scan(np, scan, E);
-                if (tid < E)
-                    for (int t = 0; t < np; ++t)
-                        passes[pex + t] =
-                            make_int4(tid, min(kPassRows, c - t * kPassRows), ex + t * kPassRows, t | (np << 16));
-                if (tid == E - 1 && n_passes) *n_passes = pex + np;
-            }
+            if (passes) write_pass_table(c, ex, E, scan, passes, n_passes);
         }
     }
     __syncthreads();
@@ -1297,15 +1307,7 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_scan(int32_t* __restr
             if (tid < E && c > 0) tprefix[na] = tex;
             if (tid == E - 1) tprefix[ntouched] = tex + nt;
         }
-        if (passes) {
-            const int np = (c + kPassRows - 1) / kPassRows;
-            const int pex = block_excl_scan(np, scan, E);
-            if (tid < E)
-                for (int t = 0; t < np; ++t)
-                    passes[pex + t] =
-                        make_int4(tid, min(kPassRows, c - t * kPassRows), ex + t * kPassRows, t | (np << 16));
-            if (tid == E - 1 && n_passes) *n_passes = pex + np;
-        }
+        if (passes) write_pass_table(c, ex, E, scan, passes, n_passes);
     }
     __syncthreads();
 
@@ -1421,7 +1423,7 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_small(const int32_t* 
     if (wave == 0) {
         const int epl = (E + 63) >> 6;  // experts per lane
         int c[kBucketSmallEpl];
-        int csum = 0, tsum = 0, psum = 0;
+        int csum = 0, tsum = 0, msum = 0, ssum = 0;
 #pragma unroll
         for (int k = 0; k < kBucketSmallEpl; ++k) {
             const int e = lane * epl + k;
@@ -1434,12 +1436,16 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_small(const int32_t* 
                 }
             csum += c[k];
             tsum += c[k] > 0 ? 1 : 0;
-            psum += (c[k] + kPassRows - 1) / kPassRows;
+            const int np = (c[k] + kPassRows - 1) / kPassRows;
+            msum += np > 1 ? np : 0;
+            ssum += np == 1 ? 1 : 0;
         }
-        int ntot, ntouched, npass;
+        // pass table order (write_pass_table): multi-chunk experts' entries first
+        int ntot, ntouched, nmulti, nsingle;
         int ex = wave_excl_scan(csum, lane, &ntot);
         int na = wave_excl_scan(tsum, lane, &ntouched);
-        int pex = wave_excl_scan(psum, lane, &npass);
+        int mex = wave_excl_scan(msum, lane, &nmulti);
+        int sex = wave_excl_scan(ssum, lane, &nsingle);
 #pragma unroll
         for (int k = 0; k < kBucketSmallEpl; ++k) {
             const int e = lane * epl + k;
@@ -1454,18 +1460,24 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_small(const int32_t* 
                     if (ce > 0) slots[na] = make_int4(e, ce, ex, 0);
                     if (e >= ntouched) slots[e] = make_int4(0, 0, 0, 0);
                 }
-                if (passes)
+                if (passes) {
+                    const int base = np > 1 ? mex : nmulti + sex;
                     for (int t = 0; t < np; ++t)
-                        passes[pex + t] =
+                        passes[base + t] =
                             make_int4(e, min(kPassRows, ce - t * kPassRows), ex + t * kPassRows, t | (np << 16));
+                }
                 ex += ce;
                 na += ce > 0 ? 1 : 0;
-                pex += np;
+                mex += np > 1 ? np : 0;
+                sex += np == 1 ? 1 : 0;
             }
         }
         if (lane == 0) {
             if (n_slots) *n_slots = ntouched;
-            if (n_passes) *n_passes = npass;
+            if (n_passes) {
+                n_passes[0] = nmulti + nsingle;
+                n_passes[1] = nmulti;
+            }
         }
     }
     __syncthreads();

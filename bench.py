@@ -167,7 +167,7 @@ def summarize(r: dict) -> dict:
             "cpu_baseline")
     out = {k: r[k] for k in keep}
     lay = r.get("layer", {})
-    for k in ("per_step_ms", "stage_ms", "hbm_gbs", "hbm_frac"):
+    for k in ("per_step_ms", "stage_ms", "batch1_launch_ms", "hbm_gbs", "hbm_frac"):
         if k in lay:
             out[k] = lay[k]
     if "transpose" in r:
@@ -313,6 +313,30 @@ def bench_layer(cfg_i: int, args, cpu_seconds: float) -> dict:
         stage_ms[j] = evs[0].elapsed_time(evs[1]) / args.steps
     assert torch.equal(out, ref_out), "staged entry points disagree with the layer entry point"
 
+    # ---- the batch-1 launches (the layer at one or two tokens): logits, gate_up with the
+    # in-kernel selection, down with the combine; each launched K times back to back
+    b1_ms = None
+    if B <= 2:
+        def b1(i, launch):
+            d = copies[i % n_copies]
+            return L.physllm_moe_stage_batch1(ctypes.byref(d.cfg), ctypes.byref(d.weights), xd.data_ptr(), B,
+                                              launch, out.data_ptr(), ws.data_ptr(), nbytes, s)
+        if b1(0, 0) == 0:
+            check(b1(0, 1))
+            check(b1(0, 2))
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref_out), "batch-1 stage launches disagree with the layer entry point"
+            b1_ms = np.zeros(3)
+            for j in range(3):
+                torch.cuda.synchronize()
+                evs[0].record(stream)
+                for i in range(args.steps):
+                    check(b1(i, j))
+                evs[1].record(stream)
+                torch.cuda.synchronize()
+                b1_ms[j] = evs[0].elapsed_time(evs[1]) / args.steps
+            assert torch.equal(out, ref_out), "batch-1 stage launches changed the output"
+
     # ---- the block around the layer (moe.rs:238-313): RMSNorm alone, then the fused
     # block entry (norm + layer + residual add) K times each, same weight rotation
     nw = torch.from_numpy(syn.bf16_from_f32(np.full(H, 1.0, np.float32)).view(np.int16)).cuda()
@@ -382,12 +406,13 @@ def bench_layer(cfg_i: int, args, cpu_seconds: float) -> dict:
                 "kernel": "gate_up grouped GEMM (k_mx_gemm3<0>)", "work_per_launch": flops}
     else:
         alg = e_touched * gu_expert_bytes + B * H * 2 + B * K * I * 2
+        # the kernel the layer call runs: at one or two tokens the batch-1 gate_up
+        if b1_ms is not None:
+            gate_up_ms = float(b1_ms[1])
         achieved = alg / (gate_up_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(cfg_i),
-                "kernel": ("gate_up grouped GEMV (the stage entry point's k_mx_gemv<0,2>; the layer call runs "
-                           "k_b1_gate_up, the same tiles after an in-kernel selection)" if B == 1 else
-                           "gate_up grouped GEMV (k_mx_gemv_stream<0>)"),
+                "kernel": ("k_b1_gate_up" if b1_ms is not None else "gate_up grouped GEMV (k_mx_gemv_stream<0>)"),
                 "work_per_launch": alg}
 
     # ---- CPU baseline (oracle on this host's cores, bounded sample) ----------------------
@@ -432,6 +457,11 @@ def bench_layer(cfg_i: int, args, cpu_seconds: float) -> dict:
                   "hbm_frac": round(layer_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                   "stage_ms": {"route": round(stage_ms[0], 5), "gate_up": round(stage_ms[1], 5),
                                "down": round(stage_ms[2], 5), "combine": round(stage_ms[3], 5)},
+                  "batch1_launch_ms": (None if b1_ms is None else
+                                       {"logits": round(float(b1_ms[0]), 5), "gate_up": round(float(b1_ms[1]), 5),
+                                        "down_combine": round(float(b1_ms[2]), 5),
+                                        "note": "the launches the layer call runs at this batch "
+                                                "(physllm_moe_stage_batch1); stage_ms times the per-stage kernels"}),
                   "block_ms": {"rms_norm": round(block_ms[0], 5), "block_forward": round(block_ms[1], 5),
                                "note": "physllm_moe_block_forward = rms_norm + layer + residual add "
                                        "fused into the combine (eager, one call per step)"},

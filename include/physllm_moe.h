@@ -167,7 +167,8 @@ PHYSLLM_MOE_API int physllm_moe_layer_forward(const physllm_moe_config* cfg, con
  * allocate device memory (code under HIP graph capture, tight serving loops); it has
  * no counterpart in the reference. It calls no allocating routine: the workspace is a
  * 64 MiB array in the library's device code object, one per device, held until the
- * process ends (looked up once per device on the first call there). A batch whose
+ * process ends (looked up once per device on the first call there: make one call on a
+ * device before capturing this entry point into a HIP graph). A batch whose
  * workspace (physllm_moe_workspace_bytes) exceeds 64 MiB is EINVAL: up to about 950
  * tokens at the GPT-OSS-20B shape, more with a smaller max_chunk_tokens. Calls that
  * overlap on one device share that array and race: order them on one stream. */
@@ -194,6 +195,18 @@ PHYSLLM_MOE_API int physllm_moe_stage_down(const physllm_moe_config* cfg, const 
 PHYSLLM_MOE_API int physllm_moe_stage_combine(const physllm_moe_config* cfg, int batch, void* out,
                               const void* topk_w, void* workspace, size_t workspace_bytes,
                               void* stream);
+
+/* The layer at one or two tokens runs as three launches when its shape allows
+ * (E <= 256, k <= 4, H and I <= 2944, 16-byte aligned x and router rows): 0 the
+ * router logits, 1 gate_up with the top-k selection made inside every workgroup,
+ * 2 down with the weighted combine. This runs launch `launch` alone on the state the
+ * earlier launches left in the workspace (0, 1, 2 in order reproduce
+ * physllm_moe_layer_forward's output bit for bit; routing stays in the workspace).
+ * It has no counterpart in the reference: it exists to time and inspect the
+ * batch-1 launches. EINVAL when the batch-1 launches do not serve cfg and batch. */
+PHYSLLM_MOE_API int physllm_moe_stage_batch1(const physllm_moe_config* cfg, const physllm_moe_weights* w,
+                             const void* x, int batch, int launch, void* out, void* workspace,
+                             size_t workspace_bytes, void* stream);
 
 /* Workspace bytes physllm_moe_block_forward needs for `batch` tokens (the layer's
  * workspace plus the normalised activations). */
@@ -233,7 +246,7 @@ PHYSLLM_MOE_API int physllm_moe_mxfp4_dequant(const void* packed, const void* sc
  * scales[f / block_size] (per element, as at :60-63). output [num_experts, in_dim,
  * out_dim] bf16 receives element f at (e*in_dim + i)*out_dim + o, bit-exact as in the
  * flat dequant. Any shape and block_size >= 1; block_size 32 with in_dim % 32 == 0,
- * out_dim % 8 == 0, 4-byte-aligned blocks and 16-byte-aligned output takes the
+ * out_dim % 8 == 0, 16-byte-aligned blocks and 16-byte-aligned output takes the
  * LDS-tiled kernel. */
 PHYSLLM_MOE_API int physllm_moe_mxfp4_dequant_transpose(const void* blocks, const void* scales, void* output,
                                         int num_experts, int out_dim, int in_dim, int block_size,

@@ -74,6 +74,8 @@ def lib() -> ctypes.CDLL:
                                        P], I),
         "physllm_moe_stage_down": ([ctypes.POINTER(MoEConfig), ctypes.POINTER(MoEWeights), I, P, SZ, P], I),
         "physllm_moe_stage_combine": ([ctypes.POINTER(MoEConfig), I, P, P, P, SZ, P], I),
+        "physllm_moe_stage_batch1": ([ctypes.POINTER(MoEConfig), ctypes.POINTER(MoEWeights), P, I, I, P, P, SZ,
+                                      P], I),
         "physllm_moe_route_topk": ([P, P, P, I, I, I, I, P, P, P], I),
         "physllm_moe_bucket": ([P, I, I, I, P, P, P, P, P], I),
         "physllm_moe_mxfp4_dequant": ([P, P, P, I64, P], I),

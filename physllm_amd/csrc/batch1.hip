@@ -333,9 +333,10 @@ bool b1_ok(int H, int I, int E, int K, int B) {
            H <= kRoute1NormMaxH && B >= 1 && B <= kB1MaxB && B * K <= kB1MaxPairs;
 }
 
-int b1_layer_launch(const B1Layer& a, hipStream_t stream) {
+int b1_layer_launch(const B1Layer& a, hipStream_t stream, int only) {
     if (!b1_ok(a.H, a.I, a.E, a.K, a.B))
         return set_error(PHYSLLM_MOE_EINVAL, "batch-1 layer: sizes out of range");
+    if (only < -1 || only > 2) return set_error(PHYSLLM_MOE_EINVAL, "batch-1 layer: launch must be 0, 1 or 2");
     static std::once_flag attr_once[kMaxDevices];
     once_per_device(attr_once, [] {
         (void)hipFuncSetAttribute((const void*)k_b1_down<kB1DownWaves>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -347,23 +348,25 @@ int b1_layer_launch(const B1Layer& a, hipStream_t stream) {
     const uint16_t* rw = (const uint16_t*)a.router_w;
     const uint16_t* rb = (const uint16_t*)a.router_b;
     const uint16_t* nw = (const uint16_t*)a.norm_w;
-    if (a.norm_w) {
-        const size_t lds = 1024 + (size_t)a.B * a.H * 2;
-        if (a.B == 1)
-            hipLaunchKernelGGL((k_b1_logits<true, false>), dim3(a.E), dim3(kB1Threads), lds, stream, rx, rw, rb, a.H,
-                               a.E, 1, a.logits, nw, a.eps, (uint16_t*)a.x);
-        else
-            hipLaunchKernelGGL((k_b1_logits<true, true>), dim3(a.E), dim3(kB1Threads), lds, stream, rx, rw, rb, a.H,
-                               a.E, a.B, a.logits, nw, a.eps, (uint16_t*)a.x);
-    } else {
-        if (a.B == 1)
-            hipLaunchKernelGGL((k_b1_logits<false, false>), dim3(a.E), dim3(64), 0, stream, rx, rw, rb, a.H, a.E, 1,
-                               a.logits, nullptr, 0.f, nullptr);
-        else
-            hipLaunchKernelGGL((k_b1_logits<false, true>), dim3(a.E), dim3(64 * a.B), 0, stream, rx, rw, rb, a.H, a.E,
-                               a.B, a.logits, nullptr, 0.f, nullptr);
+    if (only == 0 || only == -1) {
+        if (a.norm_w) {
+            const size_t lds = 1024 + (size_t)a.B * a.H * 2;
+            if (a.B == 1)
+                hipLaunchKernelGGL((k_b1_logits<true, false>), dim3(a.E), dim3(kB1Threads), lds, stream, rx, rw, rb, a.H,
+                                   a.E, 1, a.logits, nw, a.eps, (uint16_t*)a.x);
+            else
+                hipLaunchKernelGGL((k_b1_logits<true, true>), dim3(a.E), dim3(kB1Threads), lds, stream, rx, rw, rb, a.H,
+                                   a.E, a.B, a.logits, nw, a.eps, (uint16_t*)a.x);
+        } else {
+            if (a.B == 1)
+                hipLaunchKernelGGL((k_b1_logits<false, false>), dim3(a.E), dim3(64), 0, stream, rx, rw, rb, a.H, a.E, 1,
+                                   a.logits, nullptr, 0.f, nullptr);
+            else
+                hipLaunchKernelGGL((k_b1_logits<false, true>), dim3(a.E), dim3(64 * a.B), 0, stream, rx, rw, rb, a.H, a.E,
+                                   a.B, a.logits, nullptr, 0.f, nullptr);
+        }
+        if (int rc = check_launch("batch-1 logits")) return rc;
     }
-    if (int rc = check_launch("batch-1 logits")) return rc;
     B1Params p{};
     p.blocks = (const uint8_t*)a.gu_blocks;
     p.scales = (const uint8_t*)a.gu_scales;
@@ -384,14 +387,17 @@ int b1_layer_launch(const B1Layer& a, hipStream_t stream) {
     // + 256: the k-steps' edge lanes read (and discard) up to 15 units past the last row
     const int cu = a.H >> 3;
     const int n_dist = std::min(a.B * a.K, a.E);  // distinct selected experts, at most
-    if (a.B == 1) {
-        const size_t lds_gu = (size_t)kB1Hdr + 4 * kB1Slice + (size_t)cu * 16 + 256;
-        hipLaunchKernelGGL(k_b1_gate_up<1>, dim3(n_dist * p.gu_sets), dim3(kB1Threads), lds_gu, stream, p);
-    } else {
-        const size_t lds_gu = (size_t)kB1Hdr + 4 * kB1Slice + (size_t)a.B * (cu + 1) * 16 + 256;
-        hipLaunchKernelGGL(k_b1_gate_up<kB1MaxB>, dim3(n_dist * p.gu_sets), dim3(kB1Threads), lds_gu, stream, p);
+    if (only == 1 || only == -1) {
+        if (a.B == 1) {
+            const size_t lds_gu = (size_t)kB1Hdr + 4 * kB1Slice + (size_t)cu * 16 + 256;
+            hipLaunchKernelGGL(k_b1_gate_up<1>, dim3(n_dist * p.gu_sets), dim3(kB1Threads), lds_gu, stream, p);
+        } else {
+            const size_t lds_gu = (size_t)kB1Hdr + 4 * kB1Slice + (size_t)a.B * (cu + 1) * 16 + 256;
+            hipLaunchKernelGGL(k_b1_gate_up<kB1MaxB>, dim3(n_dist * p.gu_sets), dim3(kB1Threads), lds_gu, stream, p);
+        }
+        if (int rc = check_launch("batch-1 gate_up")) return rc;
     }
-    if (int rc = check_launch("batch-1 gate_up")) return rc;
+    if (only != 2 && only != -1) return PHYSLLM_MOE_OK;
     p.blocks = (const uint8_t*)a.dn_blocks;
     p.scales = (const uint8_t*)a.dn_scales;
     p.bias = (const uint16_t*)a.dn_bias;

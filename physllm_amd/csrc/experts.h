@@ -73,7 +73,10 @@ struct B1Layer {
     float alpha, limit;
 };
 bool b1_ok(int H, int I, int E, int K, int B);
-int b1_layer_launch(const B1Layer& a, hipStream_t stream);
+// The three launches of the batch-1 layer (logits, gate_up with the selection,
+// down with the combine); only = 0, 1 or 2 runs that launch alone on the state the
+// earlier ones left in the workspace, -1 runs all three.
+int b1_layer_launch(const B1Layer& a, hipStream_t stream, int only = -1);
 // RMSNorm of B rows of H bf16 values (out may equal x) and the bf16 residual add.
 int rms_norm_launch(const void* x, const void* w, void* out, int B, int H, float eps, hipStream_t stream);
 int residual_add_launch(void* out, const void* res, int64_t n, hipStream_t stream);

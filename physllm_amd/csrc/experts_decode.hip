@@ -836,8 +836,10 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
     const long stream_items = (long)((p.R + kStreamSetRows - 1) / kStreamSetRows) * max_slots * p.split;
     const bool fast = per <= 4 * kGemvNit && NB <= kStreamMaxNB;
     // The streaming kernel takes whole K rows (no split: it loads the 23 k-steps of
-    // a tile as one row segment) of experts below 2 GiB (32-bit buffer offsets).
-    const bool stream_ok = p.split == 1 && (int64_t)p.R * (p.Kdim / 2) < 0x80000000LL;
+    // a tile as one row segment) of experts below 2 GiB (32-bit buffer offsets), and
+    // copies activation rows straight into LDS in 16-byte units (16-byte aligned).
+    const bool stream_ok =
+        p.split == 1 && (int64_t)p.R * (p.Kdim / 2) < 0x80000000LL && ((uintptr_t)p.act & 15) == 0;
     if (fast && stream_ok && p.passes && max_tokens > 1 && stream_items >= 2L * n_cu) {
         // many touched experts: persistent streaming kernel, one 8-wave group per CU
         // (a multiple of 8 groups: the item order is XCD-aware)

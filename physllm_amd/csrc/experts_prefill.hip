@@ -894,8 +894,10 @@ int gemm_launch(int mode, const GemvParams& p, const int32_t* tprefix, int max_s
     const int NB = p.Kdim >> 5;
     const int tm3 = 16 * (kG3Waves / 2) * (mode == kModeGateUp ? kG3MtGateUp : kG3MtDown);
     const size_t lds3 = (size_t)g3_layout(tm3, NB).tables + (size_t)max_slots * 16 + (size_t)(max_slots + 1) * 4;
-    if (NB > 4 && NB <= kG3MaxNB && lds3 <= 160 * 1024 && ((uintptr_t)p.scales & 15) == 0 &&
-        ((uintptr_t)p.bias & 15) == 0) {
+    // k_mx_gemm3 copies activations, code blocks, scales and biases straight into LDS
+    // in 16-byte units: all four must be 16-byte aligned
+    const uintptr_t align = (uintptr_t)p.scales | (uintptr_t)p.bias | (uintptr_t)p.act | (uintptr_t)p.blocks;
+    if (NB > 4 && NB <= kG3MaxNB && lds3 <= 160 * 1024 && (align & 15) == 0) {
         // LDS-staged form: at least two k-steps; the scale and bias blocks copied in 16-byte units
         // tile heights: 384 rows for gate_up (2I = 5760 = 15 tiles at GPT-OSS shape), 320 for
         // down (H = 2880 = 9 tiles)

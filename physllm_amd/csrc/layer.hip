@@ -250,6 +250,39 @@ static bool b1_layer_path(const physllm_moe_config& c, int batch, int stages, co
     return !norm_w || (aligned16(norm_w) && aligned16(norm_x));
 }
 
+// The batch-1 layer's arguments over the workspace ws.
+static B1Layer b1_layer(const physllm_moe_config& c, const physllm_moe_weights* w, const void* x, int batch,
+                        void* out, int32_t* idx, float* wts, const Workspace& ws, const void* residual,
+                        const void* norm_w, float eps, const void* norm_x) {
+    B1Layer a{};
+    a.H = c.hidden;
+    a.I = c.intermediate;
+    a.E = c.num_experts;
+    a.K = c.top_k;
+    a.B = batch;
+    a.x = (void*)x;
+    a.norm_x = norm_x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.router_w = w->router_w;
+    a.router_b = w->router_b;
+    a.gu_blocks = w->gate_up_blocks;
+    a.gu_scales = w->gate_up_scales;
+    a.gu_bias = w->gate_up_bias;
+    a.dn_blocks = w->down_blocks;
+    a.dn_scales = w->down_scales;
+    a.dn_bias = w->down_bias;
+    a.logits = ws.lg;
+    a.h = ws.h;
+    a.idx = idx;
+    a.wts = wts;
+    a.out = out;
+    a.res = residual;
+    a.alpha = c.swiglu_alpha;
+    a.limit = c.swiglu_limit;
+    return a;
+}
+
 static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* w, const void* x, int batch,
                       void* out, void* topk_idx, void* topk_w, void* workspace, size_t workspace_bytes,
                       hipStream_t s, int stages, const void* residual = nullptr, const void* norm_w = nullptr,
@@ -271,32 +304,7 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
     float* wts = topk_w ? (float*)topk_w : ws.wts;
 
     if (b1_layer_path(c, batch, stages, x, w, norm_w, norm_x)) {
-        B1Layer a{};
-        a.H = c.hidden;
-        a.I = c.intermediate;
-        a.E = c.num_experts;
-        a.K = c.top_k;
-        a.B = batch;
-        a.x = (void*)x;
-        a.norm_x = norm_x;
-        a.norm_w = norm_w;
-        a.eps = eps;
-        a.router_w = w->router_w;
-        a.router_b = w->router_b;
-        a.gu_blocks = w->gate_up_blocks;
-        a.gu_scales = w->gate_up_scales;
-        a.gu_bias = w->gate_up_bias;
-        a.dn_blocks = w->down_blocks;
-        a.dn_scales = w->down_scales;
-        a.dn_bias = w->down_bias;
-        a.logits = ws.lg;
-        a.h = ws.h;
-        a.idx = idx;
-        a.wts = wts;
-        a.out = out;
-        a.res = residual;
-        a.alpha = c.swiglu_alpha;
-        a.limit = c.swiglu_limit;
+        const B1Layer a = b1_layer(c, w, x, batch, out, idx, wts, ws, residual, norm_w, eps, norm_x);
         if ((rc = b1_layer_launch(a, s))) return rc;
         return ok();
     }
@@ -441,6 +449,27 @@ extern "C" int physllm_moe_stage_combine(const physllm_moe_config* cfg, int batc
     if (int rc = stage_batch_ok(cfg, batch)) return rc;
     return run_stages(cfg, nullptr, nullptr, batch, out, nullptr, (void*)topk_w, workspace, workspace_bytes,
                       (hipStream_t)stream, kStageCombine);
+}
+
+// One launch of the batch-1 layer (the layer at one or two tokens, when its
+// launches fit the shape), on the state the earlier launches left in the workspace.
+extern "C" int physllm_moe_stage_batch1(const physllm_moe_config* cfg, const physllm_moe_weights* w, const void* x,
+                                        int batch, int launch, void* out, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+    if (int rc = stage_batch_ok(cfg, batch)) return rc;
+    if (batch == 0) return ok();
+    const physllm_moe_config& c = *cfg;
+    if (!w || !w->router_w || !w->gate_up_blocks || !w->gate_up_scales || !w->down_blocks || !w->down_scales)
+        return set_error(PHYSLLM_MOE_EINVAL, "stage_batch1: null weight pointer");
+    if (!x || !out) return set_error(PHYSLLM_MOE_EINVAL, "stage_batch1: null x or out");
+    if (!b1_layer_path(c, batch, kStageAll, x, w, nullptr, nullptr))
+        return set_error(PHYSLLM_MOE_EINVAL, "stage_batch1: the batch-1 launches do not serve this shape or batch");
+    if (!workspace || workspace_bytes < carve(c, batch, nullptr).bytes)
+        return set_error(PHYSLLM_MOE_EWORKSPACE, "stage_batch1: workspace too small");
+    const Workspace ws = carve(c, batch, (char*)workspace);
+    const B1Layer a = b1_layer(c, w, x, batch, out, ws.idx, ws.wts, ws, nullptr, nullptr, 0.f, nullptr);
+    if (int rc = b1_layer_launch(a, (hipStream_t)stream, launch)) return rc;
+    return ok();
 }
 
 // The MoE sub-layer of a transformer block (crates/llm-core/src/moe.rs:238-313):

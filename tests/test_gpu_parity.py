@@ -595,6 +595,35 @@ def test_layer_batch1_three_launches_equal_stages(oracle, E, H, I, K, bias):
     _check_layer(oracle, layer, x, f"batch-1 three launches E={E} H={H} I={I} K={K}")
 
 
+@pytest.mark.parametrize("B", [1, 2])
+def test_stage_batch1_launches_equal_layer(B):
+    """physllm_moe_stage_batch1 runs the batch-1 layer's launches one at a time: 0
+    (logits), 1 (selection + gate_up), 2 (down + combine) in order give the layer
+    call's output bit for bit, and launch 1 repeated on the same workspace state gives
+    the same bits again (what the bench relies on when it times it alone). A batch the
+    batch-1 launches do not serve is EINVAL, and so is a launch number past 2."""
+    layer = syn.make_layer(32, 2880, 2880, 4, seed=77 + B)
+    x = syn.make_x(B, 2880, seed=78 + B)
+    got, _, _, dl = _run_layer(layer, x)
+    L, s = capi.lib(), stream()
+    xd = dev(x)
+    ws = torch.empty(dl.workspace_bytes(B), dtype=torch.uint8, device="cuda")
+    out = torch.empty((B, 2880), dtype=torch.int16, device="cuda")
+    cfg, w = ctypes.byref(dl.cfg), ctypes.byref(dl.weights)
+    for launch in (0, 1, 1, 2):
+        assert L.physllm_moe_stage_batch1(cfg, w, xd.data_ptr(), B, launch, out.data_ptr(), ws.data_ptr(),
+                                          ws.numel(), s) == 0, capi.last_error()
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out, np.uint16), got), "batch-1 stage launches differ from the layer call"
+    assert L.physllm_moe_stage_batch1(cfg, w, xd.data_ptr(), B, 3, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                      s) == capi.PHYSLLM_MOE_EINVAL
+    x5 = dev(syn.make_x(5, 2880, seed=79))
+    ws5 = torch.empty(dl.workspace_bytes(5), dtype=torch.uint8, device="cuda")
+    out5 = torch.empty((5, 2880), dtype=torch.int16, device="cuda")
+    assert L.physllm_moe_stage_batch1(cfg, w, x5.data_ptr(), 5, 0, out5.data_ptr(), ws5.data_ptr(), ws5.numel(),
+                                      s) == capi.PHYSLLM_MOE_EINVAL
+
+
 @pytest.mark.parametrize("E,H,K,B", [(128, 256, 4, 100), (128, 2880, 4, 256), (300, 96, 8, 40), (96, 224, 2, 100),
                                      (64, 256, 4, 100), (32, 2880, 4, 64), (40, 96, 1, 17), (8, 128, 8, 127),
                                      (100, 96, 4, 300), (128, 3072, 8, 130), (65, 64, 2, 129)])
@@ -731,6 +760,56 @@ def test_layer_chunked_decode_against_oracle(oracle):
     assert np.allclose(host(w), r["wts"], rtol=1e-6, atol=1e-7)
     err = refmath.rel_l2(refmath.bf16_bits_to_f64(host(out, np.uint16)), refmath.bf16_bits_to_f64(r["out"]))
     say(f"config 2 in chunks of <= 24: rel L2 = {err:.3e}")
+    assert err < LAYER_TOL
+
+
+@pytest.mark.parametrize("B", [64, 1024])
+def test_layer_x_not_16_byte_aligned(oracle, B):
+    """x two bytes past a 16-byte boundary. The kernels that copy activation rows
+    straight into LDS in 16-byte units (the decode streaming GEMV at B = 64, the
+    LDS-staged grouped GEMM at 1024 tokens) and the router forms that load x 16 bytes at
+    a time are not taken; the fallbacks give the oracle's indices and rel L2 < 1e-2."""
+    layer = syn.make_layer(32, 2880, 2880, 4, seed=91)
+    x = syn.make_x(B, 2880, seed=92)
+    buf = torch.empty(B * 2880 + 8, dtype=torch.int16, device="cuda")
+    xv = buf[1:1 + B * 2880].view(B, 2880)
+    xv.copy_(dev(x))
+    assert xv.data_ptr() % 16 == 2
+    dl = ops.DeviceMoELayer.from_host(layer)
+    out, idx, w = ops.moe_layer_forward(dl, xv, return_routing=True)
+    torch.cuda.synchronize()
+    r = oracle.moe_layer(layer, x)
+    assert np.array_equal(host(idx), r["idx"])
+    err = refmath.rel_l2(refmath.bf16_bits_to_f64(host(out, np.uint16)), refmath.bf16_bits_to_f64(r["out"]))
+    say(f"x at 16-byte offset 2, B={B}: rel L2 = {err:.3e}")
+    assert err < LAYER_TOL
+
+
+def test_layer_automatic_chunk_limit_near_2gib(oracle):
+    """H = 32, I = 32768, k = E = 32: h [b * k, I] bf16 takes 2 MiB per token, so the
+    automatic chunk limit is 1023 tokens, whose h range (2,145,386,496 bytes) lies just
+    under the 2^31 - 2^20 bytes a 32-bit buffer range may reach; the loads meant to read
+    zeros at offset 2^31 must still land past it. 3069 tokens run as 3 automatic chunks
+    of 1023, bit-identical to 6 chunks under max_chunk_tokens = 512 (every chunk takes
+    the grouped GEMM), with rows of every chunk against the oracle."""
+    H, I, E, K = 32, 32768, 32, 32
+    layer = syn.make_layer(E, H, I, K, seed=93)
+    B = 3 * 1023
+    x = syn.make_x(B, H, seed=94)
+    dl = ops.DeviceMoELayer.from_host(layer)
+    dc = dl.with_chunk_limit(512)
+    xd = dev(x)
+    got = ops.moe_layer_forward(dl, xd, return_routing=True)
+    ref = ops.moe_layer_forward(dc, xd, return_routing=True)
+    torch.cuda.synchronize()
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b), "automatic chunks differ from 512-token chunks"
+    rows = [0, 1022, 1023, 2046, 2047, B - 1]
+    r = oracle.moe_layer(layer, x[rows])
+    assert np.array_equal(host(got[1])[rows], r["idx"])
+    err = refmath.rel_l2(refmath.bf16_bits_to_f64(host(got[0], np.uint16)[rows]),
+                         refmath.bf16_bits_to_f64(r["out"]))
+    say(f"automatic chunk limit (3 x 1023 tokens, h just under 2^31 bytes): rel L2 = {err:.3e}")
     assert err < LAYER_TOL
 
 

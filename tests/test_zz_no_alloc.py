@@ -69,3 +69,34 @@ def test_noalloc_prefill_in_chunks_and_size_limit():
     assert dc.workspace_bytes(2048) <= SCRATCH_BYTES
     check_against_workspace_entry(dc, x, "noalloc prefill 2048 in chunks of 512")
     check_against_workspace_entry(dl.with_chunk_limit(300), x[:600], "noalloc prefill 600 in chunks of 300")
+
+
+def test_noalloc_under_hip_graph_capture():
+    """After one warm-up call on the device (the array's address lookup and the kernels'
+    attributes happen on a device's first call, outside any capture), the noalloc layer
+    is captured into a HIP graph. Each replay, after new tokens are copied into the
+    captured x buffer, equals the workspace entry point's output, indices and weights on
+    those tokens, with eager work and synchronisations between the replays."""
+    layer = syn.make_layer(32, 2880, 2880, 4, seed=74)
+    dl = ops.DeviceMoELayer.from_host(layer)
+    B, K = 64, 4
+    x = torch.from_numpy(syn.make_x(B, 2880, seed=10).view(np.int16)).cuda()
+    out = torch.empty((B, 2880), dtype=torch.int16, device="cuda")
+    idx = torch.empty((B, K), dtype=torch.int32, device="cuda")
+    w = torch.empty((B, K), dtype=torch.float32, device="cuda")
+    noalloc(dl, x, out, idx, w)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        noalloc(dl, x, out, idx, w)
+    torch.cuda.synchronize()
+    for seed in (11, 12, 13, 11):
+        x.copy_(torch.from_numpy(syn.make_x(B, 2880, seed=seed).view(np.int16)).cuda())
+        g.replay()
+        torch.cuda.synchronize()
+        ref = ops.moe_layer_forward(dl, x, return_routing=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref[0]), f"graph replay (x seed {seed}): outputs differ"
+        assert torch.equal(idx, ref[1]), f"graph replay (x seed {seed}): indices differ"
+        assert torch.equal(w, ref[2]), f"graph replay (x seed {seed}): routing weights differ"
+        print(f"noalloc graph replay, x seed {seed}: identical", flush=True)

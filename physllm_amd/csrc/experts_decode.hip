@@ -109,8 +109,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv_generic(GemvParams p) 
     uint4 wq[kGemvNit];
     for (int it = 0; it < p.rt; ++it) {
         const int r0 = ((blockIdx.x * p.rt + it) * (kGemvThreads / 64) + wave) * 16;
-        if (r0 >= p.R) break;  // wave-uniform; later tiles are past the end too
-        const size_t row0 = (size_t)e * p.R + r0;
+        // the group stops together (its first tile past the end: the later ones are
+        // too); a wave whose own tile is past R (R not a multiple of 64) keeps staging
+        // its share of the activations and meeting the barriers, on tile 0's rows,
+        // and stores nothing
+        if (r0 - 16 * wave >= p.R) break;
+        const bool live = r0 < p.R;  // wave-uniform
+        const size_t row0 = (size_t)e * p.R + (live ? r0 : 0);
         const uint4* wrow = (const uint4*)(p.blocks + (row0 + m) * (size_t)(p.Kdim >> 1));
         const uint4* scg = (const uint4*)(p.scales + row0 * (size_t)NB);
         uint4 sv[kMaxScaleBlocks / 64];
@@ -138,8 +143,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv_generic(GemvParams p) 
                 const int sb1 = min(kb1, sb0 + seg_blocks);
                 if (nseg > 1) load_w(sb0, sb1);
                 if (restage || it == 0) {
-                    // every wave of the group reaches this point together: tiles past the
-                    // end only occur on the group's last iteration, where all waves stop
+                    // every wave of the group reaches this point together (those whose
+                    // tile is past R as well): the staging below is shared by all four
                     __syncthreads();  // previous pass/segment finished reading xs
                     gemv_stage<MODE>(p, xs, p0, tb, ntok, sb0, sb1, su);
                     __syncthreads();
@@ -170,7 +175,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv_generic(GemvParams p) 
                     }
                 }
             }
-            if (!tv) continue;
+            if (!tv || !live) continue;
             const f32x4_t acc = (acc0 + acc1) + (acc2 + acc3);
             const int pp = p0 + tb + m;  // sorted position of this lane's token
             const int rr = r0 + 4 * g;

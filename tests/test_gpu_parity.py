@@ -396,10 +396,13 @@ def test_layer_two_tokens_equals_stage_entry_points():
 
 
 @pytest.mark.parametrize("E,H,I,K,B", [(8, 256, 128, 3, 20), (16, 512, 1024, 4, 40), (3, 96, 160, 1, 37),
-                                       (8, 256, 4096, 2, 1), (8, 128, 3200, 2, 3)])
+                                       (8, 256, 4096, 2, 1), (8, 128, 3200, 2, 3), (5, 160, 4096, 3, 3),
+                                       (8, 160, 4096, 3, 8)])
 def test_layer_odd_shapes(oracle, E, H, I, K, B):
     """Includes down projections whose reduction (I = 4096, 3200) is split over
-    several K ranges at small batch: 128 and 100 scale blocks per row."""
+    several K ranges at small batch: 128 and 100 scale blocks per row; and with H = 160
+    rows, a last 64-row group in which only two of the four waves have a tile (the other
+    two still stage their share of the activations)."""
     layer = syn.make_layer(E, H, I, K, seed=E + B)
     x = syn.make_x(B, H, seed=B)
     _check_layer(oracle, layer, x, f"E={E} H={H} I={I} K={K} B={B}")

@@ -81,6 +81,8 @@ def parse():
                     help="with --config 0, 2, 3 or 4: the same layer at this many tokens (seeded inputs)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-baseline budget of the headline config (by_config entries get half)")
+    ap.add_argument("--hbm-probe", action="store_true",
+                    help="time device copies of 12 MB .. 1 GB, cold (rotating over 4 GiB) and hot (the same bytes)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 512 MiB device-to-device copy three times (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -99,6 +101,9 @@ def main():
 
     import torch
 
+    if args.hbm_probe:
+        hbm_probe()
+        return
     if args.calibrate_copy:
         n = 512 * 1024 * 1024
         a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
@@ -124,6 +129,36 @@ def main():
             f"roofline {by[str(c)]['roofline']['frac']}")
     res["by_config"] = by
     print(json.dumps(res), flush=True)
+
+
+def hbm_probe():
+    """Device-to-device copies of n bytes (2n bytes moved): cold rotates the source over
+    4 GiB, beyond the 256 MB Infinity Cache; hot copies the same bytes again. Median of 7
+    copies each, timed alone between HIP events. Small cold copies show the start-up cost
+    of a read from HBM that the small decode batches pay at every stage."""
+    import torch
+
+    pool = torch.empty(4 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(0)
+    rows = []
+    for mb in (12, 24, 48, 96, 240, 1000):
+        n = (mb * 1000 * 1000) // 4096 * 4096
+        for hot in (False, True):
+            off, ts = 0, []
+            for rep in range(8):
+                if not hot:
+                    off = (off + n + 37 * 4096) % (pool.numel() - n) // 4096 * 4096
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                e0.record()
+                dst[:n].copy_(pool[off:off + n])
+                e1.record()
+                e1.synchronize()
+                ts.append(e0.elapsed_time(e1))
+            med = float(np.median(ts[1:]))
+            rows.append({"mb": mb, "cache": "hot" if hot else "cold", "us": round(med * 1e3, 1),
+                         "gbs_read_plus_write": round(2 * n / (med * 1e-3) / 1e9, 1)})
+    print(json.dumps({"probe": "device copy", "rows": rows}), flush=True)
 
 
 def free_device_memory():

@@ -691,6 +691,33 @@ def test_layer_nan_activation_propagates(oracle, B):
     assert refmath.rel_l2(gf[ok], ef[ok]) < LAYER_TOL
 
 
+def _random_shapes(seed, n):
+    """Seeded layer shapes over every kernel path: E in 1..300, H and I any multiple of
+    32 up to 4096, k up to 8, decode and prefill batches, with and without biases."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        E = int(rng.choice([1, 2, 3, 5, 8, 16, 32, 33, 64, 128, 300]))
+        H = int(rng.integers(1, 129)) * 32
+        I = int(rng.integers(1, 129)) * 32
+        K = int(rng.integers(1, min(E, 8) + 1))
+        B = int(rng.choice([1, 2, 3, 5, 8, 17, 33, 64, 100, 257, 700]))
+        while B * K * H * I > 3e9 and B > 1:
+            B //= 2
+        out.append((E, H, I, K, B, bool(rng.integers(0, 2)), 1000 + i))
+    return out
+
+
+@pytest.mark.parametrize("E,H,I,K,B,bias,seed", _random_shapes(1, 40))
+def test_layer_random_shapes(oracle, E, H, I, K, B, bias, seed):
+    """Forty seeded shapes against the oracle (indices bit-exact, output within the layer
+    tolerance). Shapes like these found a last 64-row group whose idle waves skipped
+    their share of the activation staging."""
+    layer = syn.make_layer(E, H, I, K, seed=seed, with_bias=bias)
+    x = syn.make_x(B, H, seed=seed + 1000)
+    _check_layer(oracle, layer, x, f"random E={E} H={H} I={I} K={K} B={B} bias={bias}")
+
+
 def test_layer_deterministic(oracle):
     layer = syn.make_layer(32, 2880, 2880, 4, seed=21)
     x = syn.make_x(16, 2880, seed=21)

@@ -585,21 +585,26 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
         const uint32_t svoff = (uint32_t)(r0_n + m) * row_bytes + (uint32_t)g * 16u;
         const uint8_t* sl = slice0 + buf * kSliceBuf + m * NB + g;
         f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+        // the scale byte of k-step j is read two steps ahead (its LDS latency would
+        // otherwise stall every step). A lane whose block is past K (the last step of
+        // a K that is not a multiple of 128) takes the scale operand 0.0: its codes
+        // (the next row's) decode to zeros, and its staged activations past K are
+        // zeros too, so it adds exactly 0 without a per-step branch
+        uint32_t sp0 = sl[0], sp1 = sl[4];
 #pragma unroll
         for (int j = 0; j < kGemvNit; ++j) {
             if (4 * j < NB) {  // wave-uniform
-                const bool edge = 4 * j + 3 >= NB;
-                const bool bv = 4 * j + g < NB;
-                uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
+                uint32_t sj = (j & 1) ? sp1 : sp0;
+                if (4 * j + 8 < NB) {  // wave-uniform: the read for step j + 2
+                    if (j & 1) sp1 = sl[4 * j + 8];
+                    else sp0 = sl[4 * j + 8];
+                }
+                sj = 4 * j + g < NB ? sj : 0u;
                 asm volatile("" : "+v"(sj));
                 const float sf = e8m0_scale_operand(sj);
-                u32x4_t q = wq[j];
-                uint4 x0 = xrow[16 * j + xo0], x1 = xrow[16 * j + xo1], x2 = xrow[16 * j + xo2],
-                      x3 = xrow[16 * j + xo3];
-                if (edge && !bv) {
-                    q = u32x4_t{0u, 0u, 0u, 0u};
-                    x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
-                }
+                const u32x4_t q = wq[j];
+                const uint4 x0 = xrow[16 * j + xo0], x1 = xrow[16 * j + xo1], x2 = xrow[16 * j + xo2],
+                            x3 = xrow[16 * j + xo3];
                 acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
                 acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
                 acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);

@@ -49,6 +49,7 @@ constexpr int kB1MaxB = 2;         // tokens (one wave each in k_b1_logits and t
 // and ids [B][32], softmax scratch, the pairs' experts, the distinct experts
 constexpr int kB1HdrLg = 0, kB1HdrSelv = 8192, kB1HdrSeli = 9216, kB1HdrSidx = 9728, kB1HdrWl = 9856,
               kB1HdrPe = 9984, kB1HdrDist = 10048, kB1HdrNd = 10112;
+constexpr int kB1HdrZero = 10176;  // 64 zero bytes: the activations of lanes past K
 constexpr int kB1Hdr = 10240;
 
 struct B1Params {
@@ -110,26 +111,31 @@ __global__ __launch_bounds__(kB1Threads) void k_b1_logits(const uint16_t* __rest
 
 // The 23 k-steps of one 16-row tile against one token (k_mx_gemv's pass at one
 // token): wq = the tile's stripes, sl = this lane's scale row in LDS at block g,
-// xl = the token's row in LDS at block g.
+// xl = the token's row in LDS at block g, xz = 64 zero bytes in LDS. The scale byte
+// of step j is read two steps ahead (its LDS latency would stall every step); a lane
+// whose block is past K takes the scale operand 0.0 (its codes decode to zeros) and
+// reads its activations from xz, so it adds exactly 0 without a per-step branch.
 __device__ __forceinline__ f32x4_t b1_steps(const u32x4_t (&wq)[kB1Nit], const uint8_t* sl, const uint4* xl,
-                                            int nblk, int g) {
+                                            const uint4* xz, int nblk, int g) {
     f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+    uint32_t sp0 = sl[0], sp1 = sl[4];
 #pragma unroll
     for (int j = 0; j < kB1Nit; ++j) {
         if (4 * j < nblk) {  // wave-uniform
-            const bool edge = 4 * j + 3 >= nblk;
+            uint32_t sj = (j & 1) ? sp1 : sp0;
+            if (4 * j + 8 < nblk) {  // wave-uniform: the read for step j + 2
+                if (j & 1) sp1 = sl[4 * j + 8];
+                else sp0 = sl[4 * j + 8];
+            }
             const bool bv = 4 * j + g < nblk;
-            uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
+            sj = bv ? sj : 0u;
             // an opaque no-op on the scale keeps the compiler from hoisting all the
             // converted fragments ahead of the MFMAs
             asm volatile("" : "+v"(sj));
             const float sf = e8m0_scale_operand(sj);
-            u32x4_t q = wq[j];
-            uint4 x0 = xl[16 * j + 0], x1 = xl[16 * j + 1], x2 = xl[16 * j + 2], x3 = xl[16 * j + 3];
-            if (edge && !bv) {
-                q = u32x4_t{0u, 0u, 0u, 0u};
-                x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
-            }
+            const u32x4_t q = wq[j];
+            const uint4* xp = bv ? xl + 16 * j : xz;
+            const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
             acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
             acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
             acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
@@ -192,6 +198,7 @@ __global__ __launch_bounds__(kB1Threads) void k_b1_gate_up(B1Params p) {
     uint8_t* scl = (uint8_t*)(L + kB1Hdr) + wave * kB1Slice;  // this wave's tile scales [16][NB]
     uint4* xs = (uint4*)(L + kB1Hdr + 4 * kB1Slice);         // the tokens' rows [B][su]
     const int H = p.H, I = p.I, R = 2 * I, NB = H >> 5, K = p.K, B = p.B, N = B * K;
+    if (threadIdx.x < 4) ((uint4*)(L + kB1HdrZero))[threadIdx.x] = make_uint4(0, 0, 0, 0);  // (barriers below)
     const int cu = H >> 3, su = MAXB == 1 ? cu : cu + 1;  // 16-byte units per row, LDS row stride
 
     // the tokens' rows are loaded before the routing, so their latency overlaps the
@@ -263,7 +270,8 @@ __global__ __launch_bounds__(kB1Threads) void k_b1_gate_up(B1Params p) {
         }
     }
     __syncthreads();
-    const f32x4_t acc = b1_steps(tl.wq, scl + m * NB + g, xs + (MAXB == 1 ? 0 : (pm / K) * su) + 4 * g, NB, g);
+    const f32x4_t acc = b1_steps(tl.wq, scl + m * NB + g, xs + (MAXB == 1 ? 0 : (pm / K) * su) + 4 * g,
+                                 (const uint4*)(L + kB1HdrZero), NB, g);
     if (m < nu && r0 < R) {
         const int rr = r0 + 4 * g;
         const float h0 = swiglu(acc[0] + bf16_lo(tl.b2[0]), acc[1] + bf16_hi(tl.b2[0]), p.alpha, p.limit);
@@ -286,6 +294,8 @@ __global__ __launch_bounds__(64 * NW) void k_b1_down(B1Params p) {
     uint8_t* scl = (uint8_t*)lds + wave * kB1Slice;      // this wave's tile scales [16][NB]
     uint4* xs = (uint4*)((uint8_t*)lds + NW * kB1Slice);  // h rows [N][su]
     float* ys = (float*)(xs + NW * su);                   // y [N][16]
+    uint4* xz = (uint4*)(ys + NW * 16);                    // 64 zero bytes
+    if (threadIdx.x < 4) xz[threadIdx.x] = make_uint4(0, 0, 0, 0);  // (the barrier below orders it)
     const int r0 = blockIdx.x * 16;
     const int s = wave;
     const bool live = s < T * p.K && pb + s < N;
@@ -304,7 +314,7 @@ __global__ __launch_bounds__(64 * NW) void k_b1_down(B1Params p) {
         if (live && lane + 64 * u < cu) ((u32x4_t*)xs)[s * su + lane + 64 * u] = hv[u];
     __syncthreads();
     if (live) {
-        const f32x4_t acc = b1_steps(tl.wq, scl + m * NB + g, xs + s * su + 4 * g, NB, g);
+        const f32x4_t acc = b1_steps(tl.wq, scl + m * NB + g, xs + s * su + 4 * g, xz, NB, g);
         if (m == 0) {
             float* yr = ys + s * 16 + 4 * g;
             yr[0] = acc[0] + bf16_lo(tl.b2[0]);
@@ -406,12 +416,13 @@ int b1_layer_launch(const B1Layer& a, hipStream_t stream, int only) {
     p.res = (const uint16_t*)a.res;
     const int su_dn = (a.I >> 3) + 1;
     if (a.B == 1) {
-        const size_t lds_dn = (size_t)kB1MaxK * kB1Slice + (size_t)kB1MaxK * su_dn * 16 + (size_t)kB1MaxK * 16 * 4;
+        const size_t lds_dn =
+            (size_t)kB1MaxK * kB1Slice + (size_t)kB1MaxK * su_dn * 16 + (size_t)kB1MaxK * 16 * 4 + 64;
         hipLaunchKernelGGL(k_b1_down<kB1MaxK>, dim3((a.H + 15) / 16), dim3(64 * kB1MaxK), lds_dn, stream, p);
     } else {
         const int T = kB1DownWaves / a.K;  // >= 2 (k <= 4)
         const size_t lds_dn =
-            (size_t)kB1DownWaves * kB1Slice + (size_t)kB1DownWaves * su_dn * 16 + (size_t)kB1DownWaves * 16 * 4;
+            (size_t)kB1DownWaves * kB1Slice + (size_t)kB1DownWaves * su_dn * 16 + (size_t)kB1DownWaves * 16 * 4 + 64;
         hipLaunchKernelGGL(k_b1_down<kB1DownWaves>, dim3((a.H + 15) / 16, (a.B + T - 1) / T),
                            dim3(64 * kB1DownWaves), lds_dn, stream, p);
     }

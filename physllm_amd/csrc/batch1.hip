@@ -109,42 +109,6 @@ __global__ __launch_bounds__(kB1Threads) void k_b1_logits(const uint16_t* __rest
     if (lane == 0) logits[(size_t)t * E + e] = sum + b;
 }
 
-// The 23 k-steps of one 16-row tile against one token (k_mx_gemv's pass at one
-// token): wq = the tile's stripes, sl = this lane's scale row in LDS at block g,
-// xl = the token's row in LDS at block g, xz = 64 zero bytes in LDS. The scale byte
-// of step j is read two steps ahead (its LDS latency would stall every step); a lane
-// whose block is past K takes the scale operand 0.0 (its codes decode to zeros) and
-// reads its activations from xz, so it adds exactly 0 without a per-step branch.
-__device__ __forceinline__ f32x4_t b1_steps(const u32x4_t (&wq)[kB1Nit], const uint8_t* sl, const uint4* xl,
-                                            const uint4* xz, int nblk, int g) {
-    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
-    uint32_t sp0 = sl[0], sp1 = sl[4];
-#pragma unroll
-    for (int j = 0; j < kB1Nit; ++j) {
-        if (4 * j < nblk) {  // wave-uniform
-            uint32_t sj = (j & 1) ? sp1 : sp0;
-            if (4 * j + 8 < nblk) {  // wave-uniform: the read for step j + 2
-                if (j & 1) sp1 = sl[4 * j + 8];
-                else sp0 = sl[4 * j + 8];
-            }
-            const bool bv = 4 * j + g < nblk;
-            sj = bv ? sj : 0u;
-            // an opaque no-op on the scale keeps the compiler from hoisting all the
-            // converted fragments ahead of the MFMAs
-            asm volatile("" : "+v"(sj));
-            const float sf = e8m0_scale_operand(sj);
-            const u32x4_t q = wq[j];
-            const uint4* xp = bv ? xl + 16 * j : xz;
-            const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
-            acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
-            acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
-            acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
-            acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
-        }
-    }
-    return (acc0 + acc1) + (acc2 + acc3);
-}
-
 // Loads of one 16-row tile (rows r0.., all K blocks) of expert e: the scales
 // (two 16-byte loads per lane: 16 rows x NB bytes are contiguous), this lane's
 // four biases, then the 23 stripes. live = false loads nothing (empty ranges).
@@ -270,7 +234,7 @@ __global__ __launch_bounds__(kB1Threads) void k_b1_gate_up(B1Params p) {
         }
     }
     __syncthreads();
-    const f32x4_t acc = b1_steps(tl.wq, scl + m * NB + g, xs + (MAXB == 1 ? 0 : (pm / K) * su) + 4 * g,
+    const f32x4_t acc = mx_tile_steps<kB1Nit>(tl.wq, scl + m * NB + g, xs + (MAXB == 1 ? 0 : (pm / K) * su) + 4 * g,
                                  (const uint4*)(L + kB1HdrZero), NB, g);
     if (m < nu && r0 < R) {
         const int rr = r0 + 4 * g;
@@ -314,7 +278,7 @@ __global__ __launch_bounds__(64 * NW) void k_b1_down(B1Params p) {
         if (live && lane + 64 * u < cu) ((u32x4_t*)xs)[s * su + lane + 64 * u] = hv[u];
     __syncthreads();
     if (live) {
-        const f32x4_t acc = b1_steps(tl.wq, scl + m * NB + g, xs + s * su + 4 * g, xz, NB, g);
+        const f32x4_t acc = mx_tile_steps<kB1Nit>(tl.wq, scl + m * NB + g, xs + s * su + 4 * g, xz, NB, g);
         if (m == 0) {
             float* yr = ys + s * 16 + 4 * g;
             yr[0] = acc[0] + bf16_lo(tl.b2[0]);

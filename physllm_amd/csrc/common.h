@@ -70,6 +70,45 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t 
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// The k-steps of one 16-row MXFP4 tile against the B columns staged in LDS (the
+// decode GEMVs' pass): wq = the tile's stripes (step j: 16 bytes of codes of block
+// 4j + g per lane), sl = this lane's scale row in LDS at block g, xl = its
+// activation row in LDS at block g, xz = 64 zero bytes in LDS. The scale byte of
+// step j is read two steps ahead (its LDS latency would stall every step). A lane
+// whose block is past the K range takes the scale operand 0.0 (its codes decode to
+// zeros) and reads its activations from xz, so it adds exactly 0 without a per-step
+// branch. Four accumulators, summed in a fixed order.
+template <int NIT>
+__device__ __forceinline__ f32x4_t mx_tile_steps(const u32x4_t (&wq)[NIT], const uint8_t* sl, const uint4* xl,
+                                                 const uint4* xz, int nblk, int g) {
+    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
+    uint32_t sp0 = sl[0], sp1 = sl[4];
+#pragma unroll
+    for (int j = 0; j < NIT; ++j) {
+        if (4 * j < nblk) {  // wave-uniform
+            uint32_t sj = (j & 1) ? sp1 : sp0;
+            if (4 * j + 8 < nblk) {  // wave-uniform: the read for step j + 2
+                if (j & 1) sp1 = sl[4 * j + 8];
+                else sp0 = sl[4 * j + 8];
+            }
+            const bool bv = 4 * j + g < nblk;
+            sj = bv ? sj : 0u;
+            // an opaque no-op on the scale keeps the compiler from hoisting all the
+            // converted fragments ahead of the MFMAs
+            asm volatile("" : "+v"(sj));
+            const float sf = e8m0_scale_operand(sj);
+            const u32x4_t q = wq[j];
+            const uint4* xp = bv ? xl + 16 * j : xz;
+            const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+            acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
+            acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
+            acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
+            acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
+        }
+    }
+    return (acc0 + acc1) + (acc2 + acc3);
+}
+
 // ---- buffer loads -----------------------------------------------------------
 // A raw buffer over [base, base + bytes): loads past the range read zeros and
 // make no memory access.

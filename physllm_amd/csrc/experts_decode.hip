@@ -246,6 +246,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p, const in
 
     uint8_t* scl = (uint8_t*)lds + wave * kGemvSclSlice;  // this wave's tile scales [16][NB <= 92]
     uint4* xs = lds + (kGemvThreads / 64) * kGemvSclSlice / 16;  // activations [kPassTok][su]
+    uint4* xz = xs + kPassTok * (4 * per + 1);                   // 64 zero bytes (after the launch's rows)
+    if (threadIdx.x < 4) xz[threadIdx.x] = make_uint4(0, 0, 0, 0);  // (ordered by the barrier below)
 
     const __amdgpu_buffer_rsrc_t ract = make_rsrc(p.act, (uint32_t)p.act_rows * (uint32_t)p.Kdim * 2u);
     auto stage_load = [&](int tb, u32x4_t (&v)[NS]) {
@@ -312,33 +314,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_mx_gemv(GemvParams p, const in
         // read a valid row (an MFMA output column depends only on its own B column,
         // and those columns are not stored)
         const uint4* xl = xs + min(m, ntok - 1) * su + 4 * g;
-        const uint8_t* sl = scl + m * NB + kb0 + g;
-        f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
-#pragma unroll
-        for (int j = 0; j < kGemvNit; ++j) {
-            if (4 * j < nblk) {  // wave-uniform
-                const bool edge = 4 * j + 3 >= nblk;  // wave-uniform: some lanes past the K range
-                const bool bv = 4 * j + g < nblk;
-                uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
-                // decode inside the pass loop: an opaque no-op on the scale keeps the
-                // compiler from hoisting 23 x 16 VGPRs of converted fragments
-                asm volatile("" : "+v"(sj));
-                const float sf = e8m0_scale_operand(sj);
-                u32x4_t q = wq[j];
-                uint4 x0 = xl[16 * j + 0], x1 = xl[16 * j + 1], x2 = xl[16 * j + 2], x3 = xl[16 * j + 3];
-                if (edge && !bv) {
-                    q = u32x4_t{0u, 0u, 0u, 0u};
-                    x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
-                }
-                acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
-                acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
-                acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
-                acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
-            }
-        }
+        const f32x4_t acc = mx_tile_steps<kGemvNit>(wq, scl + m * NB + kb0 + g, xl, xz, nblk, g);
         const bool tv = m < ntok;
         if (!row_ok || !tv) return;
-        const f32x4_t acc = (acc0 + acc1) + (acc2 + acc3);
         const int pp = p0 + tb + m;  // sorted position of this lane's token
         const int rr = r0 + 4 * g;
         float bsum[4] = {0.f, 0.f, 0.f, 0.f};
@@ -722,6 +700,8 @@ __global__ __launch_bounds__(64 * kD1Rt * kD1MaxK) void k_mx_down1(GemvParams p,
     uint8_t* scl = (uint8_t*)lds + wave * kGemvSclSlice;          // this wave's tile scales [16][NB]
     uint4* xs = lds + (K * kD1Rt) * kGemvSclSlice / 16;          // activation rows [K][su]
     float* ys = (float*)(xs + K * su);                           // y [K][16 * kD1Rt]
+    uint4* xz = (uint4*)(ys + K * 16 * kD1Rt);                   // 64 zero bytes
+    if (threadIdx.x < 4) xz[threadIdx.x] = make_uint4(0, 0, 0, 0);  // (ordered by the barrier below)
     const int rb0 = blockIdx.x * 16 * kD1Rt;                     // first output row of the workgroup
     const int r0 = rb0 + t * 16;                                 // this wave's tile
     const int4 si = p.slots[s];                                  // {expert, 1, sorted position, 0}
@@ -754,32 +734,9 @@ __global__ __launch_bounds__(64 * kD1Rt * kD1MaxK) void k_mx_down1(GemvParams p,
     }
     __syncthreads();
     // k_mx_gemv's pass for one token (every B column reads the token's row)
-    const uint4* xl = xs + s * su + 4 * g;
-    const uint8_t* sl = scl + m * NB + g;
-    f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
-#pragma unroll
-    for (int j = 0; j < kGemvNit; ++j) {
-        if (4 * j < NB) {
-            const bool edge = 4 * j + 3 >= NB;
-            const bool bv = 4 * j + g < NB;
-            uint32_t sj = sl[edge ? (bv ? 4 * j : -g) : 4 * j];
-            asm volatile("" : "+v"(sj));
-            const float sf = e8m0_scale_operand(sj);
-            u32x4_t q = wq[j];
-            uint4 x0 = xl[16 * j + 0], x1 = xl[16 * j + 1], x2 = xl[16 * j + 2], x3 = xl[16 * j + 3];
-            if (edge && !bv) {
-                q = u32x4_t{0u, 0u, 0u, 0u};
-                x0 = x1 = x2 = x3 = make_uint4(0, 0, 0, 0);
-            }
-            acc0 = mfma16x16x32(mx_cvt8(q[0], sf), as_bf16x8(x0), acc0);
-            acc1 = mfma16x16x32(mx_cvt8(q[1], sf), as_bf16x8(x1), acc1);
-            acc2 = mfma16x16x32(mx_cvt8(q[2], sf), as_bf16x8(x2), acc2);
-            acc3 = mfma16x16x32(mx_cvt8(q[3], sf), as_bf16x8(x3), acc3);
-        }
-    }
+    const f32x4_t acc = mx_tile_steps<kGemvNit>(wq, scl + m * NB + g, xs + s * su + 4 * g, xz, NB, g);
     // column 0 holds the token: y of rows r0 + 4g .. + 3 (+ bias), into LDS
     if (m == 0) {
-        const f32x4_t acc = (acc0 + acc1) + (acc2 + acc3);
         const int rr = r0 + 4 * g;
         float bsum[4] = {0.f, 0.f, 0.f, 0.f};
         if (p.bias && rr < p.R) {
@@ -819,7 +776,7 @@ int down1_launch(const GemvParams& p, const float* wts, const int32_t* pos, uint
     });
     const int NB = p.Kdim >> 5;
     const size_t lds = (size_t)K * kD1Rt * kGemvSclSlice + (size_t)K * (4 * NB + 1) * 16 +
-                       (size_t)K * 16 * kD1Rt * sizeof(float);
+                       (size_t)K * 16 * kD1Rt * sizeof(float) + 64;
     const unsigned grid = (unsigned)((p.R + 16 * kD1Rt - 1) / (16 * kD1Rt));
     hipLaunchKernelGGL(k_mx_down1, dim3(grid), dim3(64 * kD1Rt * K), lds, stream, p, wts, pos, out, res, K);
     return check_launch("down1");
@@ -865,7 +822,7 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
         // activation units one thread stages per pass: ntok rows x 4*per 16-byte units
         const int units = ntok * 4 * per;
         const int ns = (units + kGemvThreads - 1) / kGemvThreads;
-        const size_t lds = (size_t)(kGemvThreads / 64) * kGemvSclSlice + (size_t)kPassTok * (4 * per + 1) * 16;
+        const size_t lds = (size_t)(kGemvThreads / 64) * kGemvSclSlice + (size_t)kPassTok * (4 * per + 1) * 16 + 64;
         dim3 grid(sets, max_slots, p.split);
         p.rt = 1;
         if (ns <= 2) {

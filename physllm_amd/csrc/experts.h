@@ -32,11 +32,19 @@ struct GemvParams {
     int n_pairs;             // N = batch * top_k
     int rt;                  // row-tile sets per workgroup (set by the launcher)
     float alpha, limit;
+    // streaming gate_up only (nullable): the down projection's codes [E, pf_R, pf_Kdim/2].
+    // The refills of a workgroup's last item then load the down launch's first item of
+    // the same workgroup index (the same XCD) into L2 instead of nothing.
+    const uint8_t* pf_blocks;
+    int pf_R, pf_Kdim;
 };
 
 constexpr int kMaxSplit = 4;
 constexpr int kPassRows = 16;  // tokens per pass-table entry (the MFMA's N)
 
+// Whether gemv_launch runs p on the streaming kernel (the layer's gate_up launch then
+// prefetches the down launch's first items when both stream).
+bool gemv_streams(const GemvParams& p, int max_slots, int max_tokens);
 int gemv_launch(int mode, const GemvParams& p, int max_slots, int max_tokens, hipStream_t stream);
 // out [B,H] = bf16(sum over k of w * y), then, when res is not null,
 // out = bf16(out + res) (the residual add after the layer; res may equal out).

@@ -401,6 +401,35 @@ constexpr int kStreamLds = kStreamActBytes + 2 * kStreamWaves * kStreamSlice + k
 static_assert(kStreamLds <= 160 * 1024, "streaming GEMV LDS");
 static_assert(4 * kStreamMaxNB <= kStreamActUnits && 16 * kStreamMaxNB <= kStreamSlice, "streaming GEMV tiles");
 
+// The streaming kernel's work split: workgroup rix (of G, XCD-grouped) takes items
+// f in [f0, f1) of entries ebase + f / sets (row set f % sets), given the pass table's
+// entry count npass and its nm multi-chunk entries. Returns {ebase, f0, f1}.
+__device__ __forceinline__ int3 stream_range(int npass, int nm, int G, int rix, int sets) {
+    int ebase, f0, f1;
+    // an entry of an expert with several chunks gets P workgroups of its own, each
+    // a 1/P share of its row sets; rix = part * nm + entry, so the chunks of one
+    // expert (adjacent entries) run on one XCD, start together and read the same
+    // rows at the same time (one HBM read, the rest L2 hits). The single-chunk
+    // entries share the other workgroups in contiguous ranges.
+    int P = (nm > 0 && npass <= G) ? max(1, (G + npass / 2) / npass) : 0;
+    if (P > 0) P = min(min(P, G / nm), sets);
+    if (P > 0 && npass > nm && G - P * nm < 1) P = (G - 1) / nm;
+    const int M = P * nm;
+    if (rix < M) {
+        const int part = rix / nm;
+        ebase = rix - part * nm;
+        f0 = part * sets / P;
+        f1 = (part + 1) * sets / P;
+    } else {
+        const int e0 = P > 0 ? nm : 0;
+        const int total = (npass - e0) * sets, g = G - M, r = rix - M;
+        ebase = e0;
+        f0 = (int)((int64_t)total * r / g);
+        f1 = (int)((int64_t)total * (r + 1) / g);
+    }
+    return make_int3(ebase, f0, f1);
+}
+
 template <int MODE>
 __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p, const int4* __restrict__ passes,
                                                                    const int32_t* __restrict__ perm,
@@ -413,31 +442,9 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
     const int G = (int)gridDim.x;     // a multiple of 8
     const int rix = (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3);
     // this workgroup's items f in [f0, f1): entry ebase + f / sets, row set f % sets
-    int ebase, f0, f1;
-    {
-        const int npass = n_passes[0], nm = n_passes[1];
-        // an entry of an expert with several chunks gets P workgroups of its own, each
-        // a 1/P share of its row sets; rix = part * nm + entry, so the chunks of one
-        // expert (adjacent entries) run on one XCD, start together and read the same
-        // rows at the same time (one HBM read, the rest L2 hits). The single-chunk
-        // entries share the other workgroups in contiguous ranges.
-        int P = (nm > 0 && npass <= G) ? max(1, (G + npass / 2) / npass) : 0;
-        if (P > 0) P = min(min(P, G / nm), sets);
-        if (P > 0 && npass > nm && G - P * nm < 1) P = (G - 1) / nm;
-        const int M = P * nm;
-        if (rix < M) {
-            const int part = rix / nm;
-            ebase = rix - part * nm;
-            f0 = part * sets / P;
-            f1 = (part + 1) * sets / P;
-        } else {
-            const int e0 = P > 0 ? nm : 0;
-            const int total = (npass - e0) * sets, g = G - M, r = rix - M;
-            ebase = e0;
-            f0 = (int)((int64_t)total * r / g);
-            f1 = (int)((int64_t)total * (r + 1) / g);
-        }
-    }
+    const int npass = n_passes[0], nm = n_passes[1];
+    const int3 rg = stream_range(npass, nm, G, rix, sets);
+    const int ebase = rg.x, f0 = rg.y, f1 = rg.z;
     if (f0 >= f1) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & (kStreamWaves - 1);
     const int lane = threadIdx.x & 63;
@@ -450,6 +457,22 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
     constexpr uint32_t kPast = 0x80000000u;  // an offset past every range: zeros
     lds_u8* act = (lds_u8*)lds;
     uint8_t* slice0 = (uint8_t*)lds + kStreamActBytes + wave * kStreamSlice;  // [2 buffers][4 waves][kStreamSlice]
+    // the refills of the last item: the down launch's first item for this workgroup index
+    // (stream_range with the down launch's row sets), or nothing (an empty range)
+    __amdgpu_buffer_rsrc_t pf_rs = make_rsrc(p.blocks, 0u);
+    uint32_t pf_off = 0;
+    if (MODE == kModeGateUp && p.pf_blocks) {
+        const int sets_d = (p.pf_R + kStreamSetRows - 1) / kStreamSetRows;
+        const int3 rd = stream_range(npass, nm, G, rix, sets_d);
+        if (rd.y < rd.z) {
+            const int u = rd.x + rd.y / sets_d, sd = rd.y - (rd.y / sets_d) * sets_d;
+            const int xd = __builtin_amdgcn_readfirstlane(passes[u].x);
+            const uint32_t rb_d = (uint32_t)(p.pf_Kdim >> 1);
+            const uint32_t ew_d = (uint32_t)p.pf_R * rb_d;
+            pf_rs = make_rsrc(p.pf_blocks + (size_t)xd * ew_d, ew_d);
+            pf_off = (uint32_t)(sd * kStreamSetRows + 16 * wave + m) * rb_d + (uint32_t)g * 16u;
+        }
+    }
     constexpr int kSliceBuf = kStreamWaves * kStreamSlice;
 
     // the 16 activation rows of pass entry pe into LDS: wave w copies rows 4w..4w+3,
@@ -559,8 +582,8 @@ __global__ __launch_bounds__(kStreamThreads) void k_mx_gemv_stream(GemvParams p,
         const int r0 = s * kStreamSetRows + 16 * wave;
         const int r0_n = s_n * kStreamSetRows + 16 * wave;
         side_load(pe_n.x, r0_n, has_next);
-        const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(p.blocks + (size_t)pe_n.x * exp_w, has_next ? exp_w : 0u);
-        const uint32_t svoff = (uint32_t)(r0_n + m) * row_bytes + (uint32_t)g * 16u;
+        const __amdgpu_buffer_rsrc_t rsrc = has_next ? make_rsrc(p.blocks + (size_t)pe_n.x * exp_w, exp_w) : pf_rs;
+        const uint32_t svoff = has_next ? (uint32_t)(r0_n + m) * row_bytes + (uint32_t)g * 16u : pf_off;
         const uint8_t* sl = slice0 + buf * kSliceBuf + m * NB + g;
         f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
         // the scale byte of k-step j is read two steps ahead (its LDS latency would
@@ -782,6 +805,20 @@ int down1_launch(const GemvParams& p, const float* wts, const int32_t* pos, uint
     return check_launch("down1");
 }
 
+// The streaming kernel takes whole K rows (no split: it loads the 23 k-steps of a tile
+// as one row segment) of experts below 2 GiB (32-bit buffer offsets), copies
+// activation rows straight into LDS in 16-byte units (16-byte aligned), and pays once
+// the items cover the chip twice.
+bool gemv_streams(const GemvParams& p, int max_slots, int max_tokens) {
+    const int NB = p.Kdim >> 5;
+    const int per = (NB + p.split - 1) / p.split;
+    const bool fast = per <= 4 * kGemvNit && NB <= kStreamMaxNB;
+    const bool stream_ok =
+        p.split == 1 && (int64_t)p.R * (p.Kdim / 2) < 0x80000000LL && ((uintptr_t)p.act & 15) == 0;
+    const long stream_items = (long)((p.R + kStreamSetRows - 1) / kStreamSetRows) * max_slots * p.split;
+    return fast && stream_ok && p.passes && max_tokens > 1 && stream_items >= 2L * device_cu_count();
+}
+
 int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, hipStream_t stream) {
     GemvParams p = p0;
     if (p.split < 1 || p.split > kMaxSplit) return set_error(PHYSLLM_MOE_EINVAL, "gemv: bad split");
@@ -800,14 +837,8 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
     const int rows_per_set = (kGemvThreads / 64) * 16;
     const int sets = (p.R + rows_per_set - 1) / rows_per_set;
     const int n_cu = device_cu_count();
-    const long stream_items = (long)((p.R + kStreamSetRows - 1) / kStreamSetRows) * max_slots * p.split;
     const bool fast = per <= 4 * kGemvNit && NB <= kStreamMaxNB;
-    // The streaming kernel takes whole K rows (no split: it loads the 23 k-steps of
-    // a tile as one row segment) of experts below 2 GiB (32-bit buffer offsets), and
-    // copies activation rows straight into LDS in 16-byte units (16-byte aligned).
-    const bool stream_ok =
-        p.split == 1 && (int64_t)p.R * (p.Kdim / 2) < 0x80000000LL && ((uintptr_t)p.act & 15) == 0;
-    if (fast && stream_ok && p.passes && max_tokens > 1 && stream_items >= 2L * n_cu) {
+    if (gemv_streams(p, max_slots, max_tokens)) {
         // many touched experts: persistent streaming kernel, one 8-wave group per CU
         // (a multiple of 8 groups: the item order is XCD-aware)
         const unsigned grid = (unsigned)((n_cu + 7) & ~7);

@@ -354,8 +354,24 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
         p.out = ws.h;
         p.Kdim = c.hidden;
         p.R = 2 * c.intermediate;
+        if (!use_gemm(c, batch) && (stages & kStageDown)) {
+            // when the down projection streams too, the gate_up launch's last refills
+            // prefetch its first items
+            GemvParams pd = p;
+            pd.act = ws.h;
+            pd.act_rows = N;
+            pd.Kdim = c.intermediate;
+            pd.R = c.hidden;
+            pd.split = ws.split;
+            if (gemv_streams(pd, max_slots, batch)) {
+                p.pf_blocks = (const uint8_t*)w->down_blocks;
+                p.pf_R = c.hidden;
+                p.pf_Kdim = c.intermediate;
+            }
+        }
         rc = use_gemm(c, batch) ? gemm_launch(kModeGateUp, p, ws.tprefix, max_slots, N, s)
                                 : gemv_launch(kModeGateUp, p, max_slots, batch, s);
+        p.pf_blocks = nullptr;
         if (rc) return rc;
     }
     // one token: the down projection and the combine run as one launch

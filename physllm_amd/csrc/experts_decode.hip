@@ -839,7 +839,7 @@ int gemv_launch(int mode, const GemvParams& p0, int max_slots, int max_tokens, h
     const int n_cu = device_cu_count();
     const bool fast = per <= 4 * kGemvNit && NB <= kStreamMaxNB;
     if (gemv_streams(p, max_slots, max_tokens)) {
-        // many touched experts: persistent streaming kernel, one 8-wave group per CU
+        // many touched experts: persistent streaming kernel, one 4-wave group per CU
         // (a multiple of 8 groups: the item order is XCD-aware)
         const unsigned grid = (unsigned)((n_cu + 7) & ~7);
         p.rt = 1;

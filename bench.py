@@ -5,7 +5,7 @@
 
 A step is one MoE-layer forward (router -> bucketing -> gate_up+SwiGLU -> down ->
 combine) over one batch of synthetic inputs already resident in HBM. The headline
-workload is BASELINE config 2 (GPT-OSS-20B-shape layer, decode batch 64, Zipf(1.1)
+workload is benchmark config 2 (GPT-OSS-20B-shape layer, decode batch 64, Zipf(1.1)
 router skew). To keep the 256 MB Infinity Cache from serving weights, steps rotate
 over enough device copies of the weights to exceed 1 GB. Prints ONE JSON line with
 the throughput, the dominant kernel's roofline (timed live with HIP events on the
@@ -192,7 +192,7 @@ def median_summary(runs_ms, steps: int) -> dict:
             "ms_per_step_min": round(float(np.min(runs_ms)), 5),
             "ms_per_step_max": round(float(np.max(runs_ms)), 5),
             "note": "value = K-step mean of the timed region; value_median = median over these runs of "
-                    "(run time / K), BASELINE's median of >= 20 runs; per_step_ms brackets every step "
+                    "(run time / K), the median of >= 20 runs the metric is quoted as; per_step_ms brackets every step "
                     "with its own events, which removes the launch overlap of back-to-back steps"}
 
 
@@ -298,7 +298,7 @@ def bench_layer(cfg_i: int, args, cpu_seconds: float) -> dict:
     if graphs:
         assert torch.equal(out, ref_out), "timed replays changed the output"
 
-    # ---- median of runs (BASELINE asks for the median of >= 20 runs): 21 more runs of K
+    # ---- median of runs (the metric is quoted as the median of >= 20 runs): 21 more runs of K
     # back-to-back steps, each run between its own pair of events; the run's time / K
     runs_ms = timed_runs(stream, args.steps, lambda i: graphs[i % n_copies].replay() if graphs else step(i))
 

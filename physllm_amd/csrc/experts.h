@@ -53,6 +53,12 @@ int combine_launch(const float* y, int nsplit, size_t split_stride, const int32_
 // Batch 1: down projection of the k slots and the weighted combine in one launch
 // (out = bf16(sum_j w_j * y_j) [+ res]); down1_ok says whether (K, Kdim) fit it.
 bool down1_ok(int K, int Kdim);
+// Small decode batches (N = B * k <= 24 pairs over at most 24 experts): the down
+// projection of every touched expert and the combine in one launch; downs_ok says
+// whether (pairs, slots, K, rows) fit it.
+bool downs_ok(int N, int E, int Kdim, int R);
+int downs_launch(const GemvParams& p, const float* wts, const int32_t* pos, uint16_t* out, const uint16_t* res,
+                 int B, int K, int max_slots, hipStream_t stream);
 int down1_launch(const GemvParams& p, const float* wts, const int32_t* pos, uint16_t* out, const uint16_t* res,
                  int K, hipStream_t stream);
 // Batch 1 (and 2 tokens with batch * k <= 16) in three launches: the router

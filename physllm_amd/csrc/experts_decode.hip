@@ -790,6 +790,153 @@ __global__ __launch_bounds__(64 * kD1Rt * kD1MaxK) void k_mx_down1(GemvParams p,
 
 bool down1_ok(int K, int Kdim) { return K >= 1 && K <= kD1MaxK && (Kdim >> 5) <= kD1MaxNB; }
 
+// ---------------------------------------------------------------------------
+// Small decode batches (N = B * k <= 24 routed pairs): the down projection of every
+// touched expert and the weighted combine in one launch, as k_mx_down1 does for one
+// token. Workgroup b owns output rows 16b..16b+15; wave s computes that 16-row tile of
+// slot s's expert for the slot's tokens (the MFMA columns; k_mx_gemv's tile, so the
+// same bits as the per-stage down projection without a K split); the workgroup
+// stages the N rows of h (by sorted position) once, keeps y in LDS, and each token's
+// row is combined over its k pairs in k order (k_combine's arithmetic).
+// ---------------------------------------------------------------------------
+constexpr int kDsMaxPairs = 24;  // the h rows in LDS: 24 x 5.9 KB at K = 2944
+constexpr int kDsWaves = 8;      // wave w takes slots w, w + 8, w + 16
+constexpr int kDsSlotsPerWave = 3;
+
+__global__ __launch_bounds__(64 * kDsWaves) void k_mx_downs(GemvParams p, const float* __restrict__ wts,
+                                                            const int32_t* __restrict__ pos, uint16_t* out,
+                                                            const uint16_t* res, int B, int K) {
+    extern __shared__ uint4 lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & (kDsWaves - 1);
+    const int lane = threadIdx.x & 63;
+    const int m = lane & 15, g = lane >> 4;
+    const int N = p.n_pairs;
+    const int NB = p.Kdim >> 5;
+    const int cu = NB * 4, su = cu + 1;  // activation units per row, LDS row stride
+    uint8_t* scl = (uint8_t*)lds + wave * kGemvSclSlice;          // this wave's tile scales [16][NB]
+    uint4* xs = lds + kDsWaves * kGemvSclSlice / 16;              // h rows [N][su] by sorted position
+    const int ncopy = (N * su + 63) / 64;                         // 1 KiB copies covering them
+    float* ys = (float*)(xs + 64 * ncopy);                        // y [N][16]
+    uint4* xz = (uint4*)(ys + N * 16);                            // 64 zero bytes
+    const int r0 = blockIdx.x * 16;
+    const int ns = *p.n_slots;
+    const uint32_t row_bytes = (uint32_t)(p.Kdim >> 1);
+    const uint32_t exp_w = (uint32_t)p.R * row_bytes;
+    const uint32_t exp_s = (uint32_t)p.R * (uint32_t)NB;
+    constexpr uint32_t kPast = 0x80000000u;  // an offset past every range: zeros
+    // this wave's slots (wave, wave + 8, ...): {expert, tokens, first sorted position}, read
+    // before anything else is in flight (a vector load waited on behind the copies or
+    // the stripes would wait for all of them)
+    int4 sl[kDsSlotsPerWave];
+#pragma unroll
+    for (int k = 0; k < kDsSlotsPerWave; ++k) {
+        const int sk = wave + k * kDsWaves;
+        const int4 v = sk < ns ? p.slots[sk] : make_int4(0, 0, 0, 0);
+        sl[k] = make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                          __builtin_amdgcn_readfirstlane(v.z), 0);
+    }
+    // the N rows of h into LDS by direct copies (no registers): unit d of the flattened
+    // [N][su] array from row d / su, unit d % su (the pad unit and the last copy's tail
+    // read zeros)
+    {
+        const u32x4_t ra = rsrc_words(p.act, (uint32_t)N * (uint32_t)p.Kdim * 2u);
+        for (int k = wave; k < ncopy; k += kDsWaves) {
+            const int d = 64 * k + lane;
+            const int q = d / su, c = d - q * su;
+            const uint32_t voff = (q < N && c < cu) ? (uint32_t)q * (uint32_t)(p.Kdim * 2) + (uint32_t)c * 16u : kPast;
+            dma16(ra, (const lds_u8*)(xs + 64 * k), voff);
+        }
+    }
+    if (threadIdx.x < 4) xz[threadIdx.x] = make_uint4(0, 0, 0, 0);  // (ordered by the barrier below)
+    // slot s's tile: scales into this wave's slice, then the 23 stripes
+    u32x4_t sv0, sv1, wq[kGemvNit];
+    auto tile_loads = [&](int k) {
+        const bool live = wave + k * kDsWaves < ns;
+        const int e = sl[k].x;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales + (size_t)e * exp_s, live ? exp_s : 0u);
+        const uint32_t soff = (uint32_t)r0 * NB + lane * 16u;
+        sv0 = buf_load16(rs, soff, 0);
+        sv1 = buf_load16(rs, soff, 1024);
+        __builtin_amdgcn_sched_barrier(0);
+        const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.blocks + (size_t)e * exp_w, live ? exp_w : 0u);
+        const uint32_t woff = (uint32_t)(r0 + m) * row_bytes + (uint32_t)g * 16u;
+#pragma unroll
+        for (int j = 0; j < kGemvNit; ++j) wq[j] = buf_load16(rw, 4 * j < NB ? woff : kRsrcPast, 64 * j);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    tile_loads(0);
+    // the activation copies (issued first, not counted by the compiler's waits): at most
+    // the 2 scale loads and the 23 stripes may still be in flight
+    asm volatile("s_waitcnt vmcnt(25)" ::: "memory");
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kDsSlotsPerWave; ++k) {
+        if (wave + k * kDsWaves >= ns) break;  // wave-uniform
+        ((u32x4_t*)scl)[lane] = sv0;
+        ((u32x4_t*)scl)[lane + 64] = sv1;
+        const int e = sl[k].x, nt = sl[k].y, z = sl[k].z;
+        // k_mx_gemv's pass: column m is the slot's token m (columns past its tokens
+        // compute on its first row and are not stored)
+        const uint4* xl = xs + (z + (m < nt ? m : 0)) * su + 4 * g;
+        const f32x4_t acc = mx_tile_steps<kGemvNit>(wq, scl + m * NB + g, xl, xz, NB, g);
+        if (m < nt) {
+            const int rr = r0 + 4 * g;
+            float bsum[4] = {0.f, 0.f, 0.f, 0.f};
+            if (p.bias && rr < p.R) {
+                const uint2 bb = *(const uint2*)(p.bias + (size_t)e * p.R + rr);
+                bsum[0] = bf16_lo(bb.x);
+                bsum[1] = bf16_hi(bb.x);
+                bsum[2] = bf16_lo(bb.y);
+                bsum[3] = bf16_hi(bb.y);
+            }
+            float* yr = ys + (z + m) * 16 + 4 * g;
+            yr[0] = acc[0] + bsum[0];
+            yr[1] = acc[1] + bsum[1];
+            yr[2] = acc[2] + bsum[2];
+            yr[3] = acc[3] + bsum[3];
+        }
+        if (k + 1 < kDsSlotsPerWave && wave + (k + 1) * kDsWaves < ns) tile_loads(k + 1);  // wave-uniform
+    }
+    __syncthreads();
+    // combine (k_combine's order: fmaf over the k pairs in k order, one rounding)
+    for (int i = threadIdx.x; i < B * 16; i += 64 * kDsWaves) {
+        const int t = i >> 4, rr = i & 15;
+        const int r = r0 + rr;
+        if (r < p.R) {
+            float a = 0.f;
+            for (int j = 0; j < K; ++j) a = __builtin_fmaf(wts[t * K + j], ys[pos[t * K + j] * 16 + rr], a);
+            uint32_t o = f32_to_bf16(a);
+            if (res) o = f32_to_bf16(bf16_to_f32(o) + bf16_to_f32(res[(size_t)t * p.R + r]));
+            out[(size_t)t * p.R + r] = (uint16_t)o;
+        }
+    }
+}
+
+bool downs_ok(int N, int E, int Kdim, int R) {
+    const int slots = N < E ? N : E;
+    const size_t lds = (size_t)kDsWaves * kGemvSclSlice + ((size_t)N * (4 * (Kdim >> 5) + 1) + 63) / 64 * 1024 +
+                       (size_t)N * 64 + 64;
+    return N >= 1 && N <= kDsMaxPairs && slots <= kDsSlotsPerWave * kDsWaves && (Kdim >> 5) <= kStreamMaxNB &&
+           R % 16 == 0 && lds <= 160 * 1024;
+}
+
+int downs_launch(const GemvParams& p, const float* wts, const int32_t* pos, uint16_t* out, const uint16_t* res,
+                 int B, int K, int max_slots, hipStream_t stream) {
+    if (!downs_ok(p.n_pairs, max_slots, p.Kdim, p.R)) return set_error(PHYSLLM_MOE_EINVAL, "downs: sizes out of range");
+    static std::once_flag attr_once[kMaxDevices];
+    once_per_device(attr_once, [] {
+        (void)hipFuncSetAttribute((const void*)k_mx_downs, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    });
+    const int NB = p.Kdim >> 5;
+    const size_t ncopy = ((size_t)p.n_pairs * (4 * NB + 1) + 63) / 64;
+    const size_t lds = (size_t)kDsWaves * kGemvSclSlice + ncopy * 64 * 16 + (size_t)p.n_pairs * 16 * sizeof(float) + 64;
+    const unsigned grid = (unsigned)((p.R + 15) / 16);
+    hipLaunchKernelGGL(k_mx_downs, dim3(grid), dim3(64 * kDsWaves), lds, stream, p, wts, pos, out, res, B, K);
+    return check_launch("downs");
+}
+
+
+
 int down1_launch(const GemvParams& p, const float* wts, const int32_t* pos, uint16_t* out, const uint16_t* res,
                  int K, hipStream_t stream) {
     if (!down1_ok(K, p.Kdim)) return set_error(PHYSLLM_MOE_EINVAL, "down1: sizes out of range");

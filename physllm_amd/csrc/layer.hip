@@ -374,9 +374,11 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
         p.pf_blocks = nullptr;
         if (rc) return rc;
     }
-    // one token: the down projection and the combine run as one launch
-    const bool down1 = batch == 1 && (stages & kStageDown) && (stages & kStageCombine) && !use_gemm(c, batch) &&
-                       down1_ok(c.top_k, c.intermediate);
+    // one token, and small batches (at most 24 routed pairs): the down projection and
+    // the combine run as one launch
+    const bool fuse = (stages & kStageDown) && (stages & kStageCombine) && !use_gemm(c, batch);
+    const bool down1 = fuse && batch == 1 && down1_ok(c.top_k, c.intermediate);
+    const bool downs = fuse && batch >= 2 && downs_ok(N, max_slots, c.intermediate, c.hidden);
     if (stages & kStageDown) {
         p.act = ws.h;
         p.act_rows = N;
@@ -390,13 +392,16 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
         if (down1) {
             p.split = 1;
             rc = down1_launch(p, wts, ws.pos, (uint16_t*)out, (const uint16_t*)residual, c.top_k, s);
+        } else if (downs) {
+            p.split = 1;
+            rc = downs_launch(p, wts, ws.pos, (uint16_t*)out, (const uint16_t*)residual, batch, c.top_k, max_slots, s);
         } else {
             rc = use_gemm(c, batch) ? gemm_launch(kModeDown, p, ws.tprefix, max_slots, N, s)
                                     : gemv_launch(kModeDown, p, max_slots, batch, s);
         }
         if (rc) return rc;
     }
-    if ((stages & kStageCombine) && !down1) {
+    if ((stages & kStageCombine) && !down1 && !downs) {
         if ((rc = combine_launch(ws.y, ws.split, (size_t)N * c.hidden, ws.pos, wts, (uint16_t*)out,
                                  (const uint16_t*)residual, batch, c.hidden, c.top_k, s)))
             return rc;

@@ -184,13 +184,15 @@ def _separate_calls(dl, x, nw, eps):
     return host(m, np.uint16)
 
 
-@pytest.mark.parametrize("E,H,I,K,B", [(4, 64, 64, 2, 3), (8, 256, 128, 3, 20), (32, 2880, 2880, 4, 1),
+@pytest.mark.parametrize("E,H,I,K,B", [(4, 64, 64, 2, 3), (32, 2880, 2880, 4, 4), (32, 2880, 2880, 4, 6), (8, 256, 128, 3, 20),
+                                       (32, 2880, 2880, 4, 1),
                                        (8, 256, 128, 3, 1), (200, 96, 64, 5, 1), (32, 2880, 2880, 4, 2),
                                        (4, 64, 64, 2, 2), (128, 2880, 2880, 4, 2),
                                        (32, 2880, 2880, 4, 64), (4, 256, 128, 2, 512), (128, 256, 128, 4, 2048)])
 def test_block_forward(oracle, E, H, I, K, B):
-    """Batch 1 and 2 (the norm runs inside the logits launch), decode GEMV, grouped
-    GEMM (512 tokens on 4 experts) and the two-pass router (2048 tokens, 128 experts)."""
+    """Batch 1 and 2 (the norm runs inside the logits launch), 3, 4 and 6 (the residual
+    add inside the fused down + combine launch), decode GEMV, grouped GEMM (512 tokens on 4
+    experts) and the two-pass router (2048 tokens, 128 experts)."""
     say(f"block E={E} H={H} I={I} K={K} B={B}")
     layer = syn.make_layer(E, H, I, K, seed=E + B)
     x = syn.make_x(B, H, seed=B + 1)

@@ -793,6 +793,33 @@ def test_layer_chunked_decode_against_oracle(oracle):
     assert err < LAYER_TOL
 
 
+@pytest.mark.parametrize("E,H,I,K,B,bias", [(32, 2880, 2880, 4, 3, True), (32, 2880, 2880, 4, 4, False),
+                                            (128, 2944, 2944, 4, 4, True), (8, 2048, 512, 2, 5, True),
+                                            (16, 2560, 1280, 1, 16, True), (32, 2880, 2880, 4, 5, False),
+                                            (32, 2880, 2880, 4, 6, True), (128, 2944, 2944, 4, 6, True),
+                                            (64, 2048, 2048, 1, 24, True)])
+def test_layer_small_batch_fused_down_equals_stages(oracle, E, H, I, K, B, bias):
+    """Decode batches of at most 24 routed pairs run the down projection and the combine
+    as one launch (k_mx_downs). Where the per-stage down projection does not split K (at
+    least 512 16-row tiles), the layer's output equals the per-stage entry points' bit for
+    bit; everywhere it matches the oracle, and repeated calls give the same bits. The
+    block (norm + layer + residual add in the same launch) is checked against the oracle
+    block as well."""
+    layer = syn.make_layer(E, H, I, K, seed=E * 7 + B, with_bias=bias)
+    x = syn.make_x(B, H, seed=H + B)
+    got, gidx, gw, dl = _run_layer(layer, x)
+    sout, sidx, sw = _run_stages(dl, dev(x), B)
+    assert np.array_equal(gidx, sidx) and np.array_equal(gw.view(np.uint32), sw.view(np.uint32))
+    tiles = min(B * K, E) * (H // 16)
+    if tiles >= 512:
+        assert np.array_equal(got, sout), "fused down + combine differs from the per-stage path"
+    for _ in range(2):
+        again, _, _ = ops.moe_layer_forward(dl, dev(x), return_routing=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(again, np.uint16), got)
+    _check_layer(oracle, layer, x, f"fused small-batch down E={E} H={H} I={I} K={K} B={B}")
+
+
 @pytest.mark.parametrize("B", [64, 1024])
 def test_layer_x_not_16_byte_aligned(oracle, B):
     """x two bytes past a 16-byte boundary. The kernels that copy activation rows

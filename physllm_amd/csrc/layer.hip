@@ -318,7 +318,8 @@ static int run_stages(const physllm_moe_config* cfg, const physllm_moe_weights* 
                                ws.n_passes, s, norm_w, eps, norm_w ? (void*)x : nullptr);
         } else if (!gemm && dec_route_ok(batch, c.num_experts, c.top_k) && c.hidden % 8 == 0 && aligned16(x) &&
                    aligned16(w->router_w)) {
-            // decode at small B * E: logits over many waves, then selection + bucketing in one launch
+            // decode at small B * E: logits over many waves, one selection workgroup per
+            // token, then the one-workgroup bucketing
             rc = dec_route_launch(x, w->router_w, w->router_b, batch, c.hidden, c.num_experts, c.top_k, ws.lg, idx,
                                   wts, ws.counts, ws.offsets, ws.perm, ws.pos, ws.slots, ws.n_slots, ws.passes,
                                   ws.n_passes, s);

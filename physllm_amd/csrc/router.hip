@@ -703,20 +703,22 @@ __global__ __launch_bounds__(kRmxThreads) void k_rmx_bounds(const uint16_t* __re
     }
 }
 
-constexpr int kRsWaves = 2;  // tokens (one per wave) per selection workgroup: spread over the CUs
+// waves per token in the tiled router's selection: each computes the threshold and the
+// candidate list, then the exact logits of its share of the candidate pairs (a token's
+// 5-10 candidates in one round of loads instead of 3-5 in a row)
+constexpr int kRsSplit = 4;
 
-__global__ __launch_bounds__(64 * kRsWaves) void k_rmx_select(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(64 * kRsSplit) void k_rmx_select(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ w,
                                                             const uint16_t* __restrict__ bias, int B, int H, int E,
                                                             int K, const float2* __restrict__ lohi,
                                                             int32_t* __restrict__ idx, float* __restrict__ wts) {
-    __shared__ double exact[kRsWaves][kRmxMaxE];
-    __shared__ int32_t cand[kRsWaves][kRmxMaxE];
-    __shared__ double selv[kRsWaves][32];
-    __shared__ int32_t seli[kRsWaves][32];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t = blockIdx.x * kRsWaves + wave;
-    if (t >= B) return;  // no workgroup barriers below
+    __shared__ double exact[kRmxMaxE];
+    __shared__ int32_t cand[kRsSplit][kRmxMaxE];  // the same list from every wave
+    __shared__ double selv[32];
+    __shared__ int32_t seli[32];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int t = blockIdx.x;  // one workgroup per token (grid = B)
     const float2* lh = lohi + (size_t)t * E;
     const bool v0 = lane < E, v1 = lane + 64 < E;
     const float2 q0 = v0 ? lh[lane] : make_float2(0.f, 0.f);
@@ -751,7 +753,8 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_rmx_select(const uint16_t* __
     if (c0) cand[wave][__popcll(m0 & lt)] = lane;
     if (c1) cand[wave][n0 + __popcll(m1 & lt)] = lane + 64;
     __builtin_amdgcn_wave_barrier();
-    // exact logits of the candidates, two at a time (k_router's lane order)
+    // exact logits of the candidates, two at a time (k_router's lane order): wave w takes
+    // pairs 2w, 2w + 2 * kRsSplit, ...
     const int nch = H >> 3;
     const uint4* xr = (const uint4*)(x + (size_t)t * H);
     uint4 xv[6];
@@ -760,7 +763,7 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_rmx_select(const uint16_t* __
         const int c = lane + 64 * i;
         xv[i] = c < nch ? xr[c] : make_uint4(0, 0, 0, 0);
     }
-    for (int j = 0; j < nc; j += 2) {
+    for (int j = 2 * wave; j < nc; j += 2 * kRsSplit) {
         const bool hb = j + 1 < nc;
         const int ea = cand[wave][j], eb = cand[wave][hb ? j + 1 : j];
         const uint4* wa = (const uint4*)(w + (size_t)ea * H);
@@ -786,16 +789,17 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_rmx_select(const uint16_t* __
         }
         const double ra = wave_sum_f64(sa), rb = wave_sum_f64(sb);
         if (lane == 0) {
-            exact[wave][j] = ra + (bias ? (double)bf16_to_f32(bias[ea]) : 0.0);
-            if (hb) exact[wave][j + 1] = rb + (bias ? (double)bf16_to_f32(bias[eb]) : 0.0);
+            exact[j] = ra + (bias ? (double)bf16_to_f32(bias[ea]) : 0.0);
+            if (hb) exact[j + 1] = rb + (bias ? (double)bf16_to_f32(bias[eb]) : 0.0);
         }
     }
+    __syncthreads();  // every candidate's exact logit is in LDS
+    if (wave != 0) return;
+    ballot_select(exact, nc, K, 0, 1, lane, seli, selv);
     __builtin_amdgcn_wave_barrier();
-    ballot_select(exact[wave], nc, K, 0, 1, lane, seli[wave], selv[wave]);
+    if (lane < K) seli[lane] = cand[0][seli[lane]];
     __builtin_amdgcn_wave_barrier();
-    if (lane < K) seli[wave][lane] = cand[wave][seli[wave][lane]];
-    __builtin_amdgcn_wave_barrier();
-    softmax_selected(seli[wave], selv[wave], K, lane, idx + (size_t)t * K, wts + (size_t)t * K);
+    softmax_selected(seli, selv, K, lane, idx + (size_t)t * K, wts + (size_t)t * K);
 }
 
 int router_launch(const void* x, const void* w, const void* bias, int B, int H, int E, int K, void* idx,
@@ -808,13 +812,13 @@ int router_launch(const void* x, const void* w, const void* bias, int B, int H, 
     const int vec = (H % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0);
     if (lg_ws && rmx_tiled(B, E) && H % 32 == 0 && H <= kRmxMaxH && vec) {
         // inside the layer, E > 64: the tiled two-pass router (bounds into the workspace);
-        // at config 4 it takes 23 us against 30 for the two-launch exact router, while
-        // with E <= 64 (config 3) k_router_mx is as fast in one launch
+        // at config 4 the route stage takes 20 us against 30 for the two-launch exact
+        // router, while with E <= 64 (config 3) k_router_mx is as fast in one launch
         hipLaunchKernelGGL(k_rmx_bounds, dim3((B + kRmxTok - 1) / kRmxTok, (E + 15) / 16), dim3(kRmxThreads), 0,
                            stream, (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, B, H, E,
                            (float2*)lg_ws);
         if (int rc = check_launch("router bounds")) return rc;
-        hipLaunchKernelGGL(k_rmx_select, dim3((B + kRsWaves - 1) / kRsWaves), dim3(64 * kRsWaves), 0, stream,
+        hipLaunchKernelGGL(k_rmx_select, dim3(B), dim3(64 * kRsSplit), 0, stream,
                            (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, B, H, E, K,
                            (const float2*)lg_ws, (int32_t*)idx, (float*)wts);
     } else if (B >= kRmxMinBatch && E <= kRmxMaxE && H % 32 == 0 && H <= kRmxMaxH && vec &&

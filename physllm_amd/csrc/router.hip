@@ -1426,18 +1426,30 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_small(const int32_t* 
     __syncthreads();
     if (wave == 0) {
         const int epl = (E + 63) >> 6;  // experts per lane
+        constexpr int kW = kBucketThreads / 64;
+        // every wave's count of this lane's experts first (one LDS wait, not one per
+        // wave), then the waves' starts in their place
+        int v[kBucketSmallEpl][kW];
+#pragma unroll
+        for (int k = 0; k < kBucketSmallEpl; ++k) {
+            const int e = lane * epl + k;
+            const int ec = (k < epl && e < E) ? e : 0;  // unconditional reads (the sums below skip the rest)
+#pragma unroll
+            for (int w2 = 0; w2 < kW; ++w2) v[k][w2] = wcnt[w2 * E + ec];
+        }
         int c[kBucketSmallEpl];
         int csum = 0, tsum = 0, msum = 0, ssum = 0;
 #pragma unroll
         for (int k = 0; k < kBucketSmallEpl; ++k) {
             const int e = lane * epl + k;
             c[k] = 0;
-            if (k < epl && e < E)
-                for (int w2 = 0; w2 < kBucketThreads / 64; ++w2) {
-                    const int x = wcnt[w2 * E + e];
+            if (k < epl && e < E) {
+#pragma unroll
+                for (int w2 = 0; w2 < kW; ++w2) {
                     wcnt[w2 * E + e] = c[k];
-                    c[k] += x;
+                    c[k] += v[k][w2];
                 }
+            }
             csum += c[k];
             tsum += c[k] > 0 ? 1 : 0;
             const int np = (c[k] + kPassRows - 1) / kPassRows;

@@ -636,8 +636,9 @@ def test_layer_two_launch_router(oracle, E, H, K, B):
     workgroup per token); the smaller ones here take k_router. Indices bit-exact and
     weights as the oracle's, with ties to the lower index, a NaN token, more than 256
     experts (arg-max rounds), k = 1 and k = E. Batches of 128 or more with 64 < E <= 128
-    take the tiled two-pass router (bounds per 16 x 16 tile, then one selection wave
-    per token), including expert counts that are not multiples of 16."""
+    take the tiled two-pass router (bounds per 16 x 16 tile, then one 4-wave selection
+    workgroup per token; the NaN token makes every expert a candidate, spread over its
+    four waves), including expert counts that are not multiples of 16."""
     layer = syn.make_layer(E, H, 64, K, seed=E + B)
     tie = [2, 5, 9] if E > 9 else [1, 3, 5]
     rw = layer.router_w.copy()

@@ -1118,10 +1118,17 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_waves(const int32_t* 
     } else {
         for (int e = tid; e < E; e += kBucketThreads) {
             int run = 0;
-            for (int w2 = 0; w2 < nwaves; ++w2) {
-                const int c = wcnt[w2 * E + e];
-                wcnt[w2 * E + e] = run;
-                run += c;
+            for (int w0 = 0; w0 < nwaves; w0 += 8) {  // eight counts read per LDS wait
+                int v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = wcnt[min(w0 + i, nwaves - 1) * E + e];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if (w0 + i < nwaves) {
+                        wcnt[(w0 + i) * E + e] = run;
+                        run += v[i];
+                    }
+                }
             }
             cnt[e] = run;
         }
@@ -1282,11 +1289,20 @@ __global__ __launch_bounds__(kBucketThreads) void k_bucket_scan(int32_t* __restr
     if (j < T) part[j * E + e] = sum;
     __syncthreads();
     if (tid < E) {
+        // eight part sums read before their prefixes are written back (one LDS wait
+        // per eight, not one per part)
         int run = 0;
-        for (int j2 = 0; j2 < T; ++j2) {
-            const int c = part[j2 * E + tid];
-            part[j2 * E + tid] = run;
-            run += c;
+        for (int j0 = 0; j0 < T; j0 += 8) {
+            int v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = part[min(j0 + i, T - 1) * E + tid];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (j0 + i < T) {
+                    part[(j0 + i) * E + tid] = run;
+                    run += v[i];
+                }
+            }
         }
         tot[tid] = run;
     }

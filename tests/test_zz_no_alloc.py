@@ -40,11 +40,12 @@ def check_against_workspace_entry(dl, x, label):
 
 
 def test_noalloc_equals_workspace_entry_on_shrinking_calls():
-    """GPT-OSS-20B shape: decode B = 64 (streaming GEMV), then B = 8, 2 and 1 (smaller
-    inputs into the same array; 2 and 1 take the three-launch path), then B = 64 again."""
+    """GPT-OSS-20B shape: decode B = 64 (streaming GEMV), then B = 8, 4, 2 and 1 (smaller
+    inputs into the same array; 4 runs the down projection and the combine as one
+    launch, 2 and 1 take the three-launch path), then B = 64 again."""
     layer = syn.make_layer(32, 2880, 2880, 4, seed=71)
     dl = ops.DeviceMoELayer.from_host(layer)
-    for B, seed in ((64, 1), (8, 2), (2, 5), (1, 3), (64, 4)):
+    for B, seed in ((64, 1), (8, 2), (4, 6), (2, 5), (1, 3), (64, 4)):
         x = torch.from_numpy(syn.make_x(B, 2880, seed=seed).view(np.int16)).cuda()
         assert dl.workspace_bytes(B) <= SCRATCH_BYTES
         check_against_workspace_entry(dl, x, f"noalloc B={B}")
